@@ -1,0 +1,246 @@
+"""Benchmark of torch.ops.vectra.rbf_attention on one MI355X.
+
+  python bench.py [--steps K] [--warmup W] [--config serving]
+
+A step is one call of the operator over one batch of the configuration
+(default: the serving shape B=1024, H=8, Lq=1, Lk=64, D=32, bf16, per-head
+gamma, ragged key-padding masks).  Inputs are resident in HBM before timing.
+Each step reads a different one of R input sets whose total exceeds the
+256 MB Infinity Cache, so every launch streams its K and V from HBM.
+
+Numerics are gated before anything is timed: the fp32 output of the same
+kernel must match the eager chain (the CPU baseline below) within rtol 1e-3 /
+atol 1e-4 (bf16/fp16 inputs) or 1e-5 / 1e-6 (fp32), and the operator's
+v.dtype output must be exactly that fp32 result rounded once.
+
+The K timed steps are one HIP-graph replay of K operator launches (host
+launch overhead is not the GPU's throughput), bracketed by
+torch.cuda.synchronize() and events on the stream the kernels run on.
+
+Prints one JSON line:  queries/s (value), ms_per_step, the roofline of the
+kernel (algorithmic bytes / average launch time vs 8 TB/s) and the CPU
+baseline (the eager chain, torch fp32, on the host cores).
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from vectra_amd.benchmarks import configs  # noqa: E402
+from vectra_amd.benchmarks import roofline  # noqa: E402
+from vectra_amd.kernels import _native  # noqa: E402
+from vectra_amd.kernels import capi  # noqa: E402
+import vectra_amd.kernels  # noqa: E402,F401  (registers the operator)
+
+# Input sets rotate over at least this many bytes (> the 256 MB MALL).
+ROTATION_BYTES = 320 << 20
+MIN_SETS = 5
+
+KERNEL_NAMES = {
+    'stream': 'rbf_stream_kernel',
+    'generic': 'rbf_generic_kernel',
+    'mfma': 'rbf_mfma_kernel',
+}
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split('\n\n')[0])
+    p.add_argument('--gpus', type=int, default=1)
+    p.add_argument('--steps', type=int, default=200)
+    p.add_argument('--warmup', type=int, default=20)
+    p.add_argument('--config', default='serving', choices=sorted(configs.CONFIGS))
+    p.add_argument('--dtype', default=None, choices=['bf16', 'fp16', 'fp32'])
+    p.add_argument('--no-graph', action='store_true', help='time a host loop instead of a graph')
+    p.add_argument('--cpu-seconds', type=float, default=12.0,
+                   help='CPU-baseline budget (0 skips the CPU leg; numerics then use the '
+                   'bit-exact rounding check only)')
+    p.add_argument('--sets', type=int, default=0, help='input sets to rotate (0: auto)')
+    return p.parse_args()
+
+
+def cpu_baseline(config, host_inputs, seconds):
+    """Times the eager chain (the oracle's restatement of the reference's
+    reference.py:54-58) in torch fp32 on the host cores; returns (record,
+    output on the sample)."""
+    from oracle import rbf as oracle  # noqa: E402  (cpu_baseline leg only)
+
+    threads = torch.get_num_threads()
+    sample = host_inputs
+    chunk = 64 if config.n_q > 1 else None
+    out = oracle.eager_fp32(*sample.args(), batch_chunk=chunk)  # warm-up + reference
+    reps, start = 0, time.perf_counter()
+    while True:
+        oracle.eager_fp32(*sample.args(), batch_chunk=chunk)
+        reps += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= seconds:
+            break
+    qps = sample.q.shape[0] * reps / elapsed
+    cpu_model = 'unknown'
+    try:
+        with open('/proc/cpuinfo', encoding='utf-8') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    cpu_model = line.split(':', 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    record = {
+        'value': qps,
+        'unit': 'queries/s',
+        'cores': threads,
+        'kind': 'port',
+        'sample': (
+            f'eager chain (sub, pow, sum, scale, bias, softmax, matmul) in torch fp32 on '
+            f'{sample.q.shape[0]} subjects of input set 0 (bf16 inputs upcast), '
+            f'{reps} reps in {elapsed:.1f}s on {threads} threads of {cpu_model}'
+        ),
+    }
+    return record, out
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f'bench.py measures one GPU; --gpus {args.gpus} is not supported '
+            '(the operator shards over batches with no exchange between GPUs).',
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print('bench.py needs a GPU', file=sys.stderr)
+        sys.exit(1)
+
+    config = configs.CONFIGS[args.config]
+    if args.dtype:
+        config = config.with_dtype({'bf16': torch.bfloat16, 'fp16': torch.float16,
+                                    'fp32': torch.float32}[args.dtype])
+    shape = config.shape()
+    host0 = configs.make_inputs(config, seed=0)
+    per_set = host0.nbytes()
+    n_sets = args.sets or max(MIN_SETS, math.ceil(ROTATION_BYTES / per_set))
+    log(f'config {config.name}: {per_set / 1e6:.1f} MB per input set, rotating {n_sets} sets')
+    sets = [host0.to('cuda')] + [
+        configs.make_inputs(config, seed=s).to('cuda') for s in range(1, n_sets)
+    ]
+    torch.cuda.synchronize()
+
+    # ---- CPU baseline leg (also the numerics reference). ----
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu, want = cpu_baseline(config, host0, args.cpu_seconds)
+        log(f'cpu baseline: {cpu["value"]:.4g} queries/s on {cpu["cores"]} threads')
+
+    # ---- Numerics gate (before any timing). ----
+    fp32 = capi.forward(*sets[0].args(), out_dtype=torch.float32)
+    out = torch.ops.vectra.rbf_attention(*sets[0].args())
+    torch.cuda.synchronize()
+    if not torch.equal(out, fp32.to(out.dtype)):
+        raise SystemExit('numerics gate: operator output is not the rounded fp32 result')
+    if cpu is not None:
+        tol = (1e-5, 1e-6) if config.dtype == torch.float32 else (1e-3, 1e-4)
+        torch.testing.assert_close(fp32.cpu(), want, rtol=tol[0], atol=tol[1], equal_nan=True)
+        log('numerics gate passed against the eager chain')
+
+    probe = capi.make_args(*[t for t in (sets[0].q, sets[0].k, sets[0].v)], fp32,
+                           *capi.broadcast_operands(sets[0].q, sets[0].k, sets[0].scale,
+                                                    sets[0].key_bias))
+    variant = capi.VARIANT_NAMES[capi.select_variant(probe)]
+
+    def step(i):
+        return torch.ops.vectra.rbf_attention(*sets[i % n_sets].args())
+
+    stream = torch.cuda.current_stream()
+    if args.no_graph:
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(args.steps):
+            step(i)
+        end.record(stream)
+        torch.cuda.synchronize()
+    else:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for i in range(3):
+                step(i)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        warm, timed = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(warm):
+            for i in range(max(args.warmup, 1)):
+                step(i)
+        with torch.cuda.graph(timed):
+            for i in range(args.steps):
+                step(i)
+        warm.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        timed.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+
+    ms = start.elapsed_time(end) / args.steps
+    seconds = ms / 1e3
+    fused = roofline.fused_bytes(shape)
+    mfma_bound = config.n_q >= 1024
+    if mfma_bound:
+        achieved = roofline.matrix_flops(shape) / seconds / 1e12
+        line_roof = {'bound': 'mfma', 'achieved': achieved,
+                     'peak': roofline.MI355X.bf16_mfma_flops / 1e12, 'unit': 'TFLOP/s'}
+    else:
+        achieved = fused / seconds / 1e9
+        line_roof = {'bound': 'hbm', 'achieved': achieved,
+                     'peak': roofline.MI355X.hbm_bytes_per_s / 1e9, 'unit': 'GB/s'}
+    line_roof['frac'] = line_roof['achieved'] / line_roof['peak']
+    line_roof['traffic'] = None
+    line_roof['kernel'] = KERNEL_NAMES.get(variant, variant)
+    line_roof['algorithmic_bytes'] = fused
+
+    result = {
+        'metric': 'rbf_attention queries/s + % of HBM peak at B=1024 serving shape, bf16',
+        'value': config.batch / seconds,
+        'unit': 'queries/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': ms,
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': {torch.bfloat16: 'bf16', torch.float16: 'fp16', torch.float32: 'fp32'}[config.dtype],
+        'data': 'synthetic',
+        'config': {
+            'workload': f'{config.name}: B={config.batch} H={config.heads} Lq={config.n_q} '
+                        f'Lk={config.n_k} D={config.head_dim}',
+            'batch': config.batch, 'heads': config.heads, 'n_q': config.n_q, 'n_k': config.n_k,
+            'head_dim': config.head_dim, 'input_sets': n_sets,
+            'timing': 'host loop' if args.no_graph else 'hip graph of K launches',
+            'variant': variant,
+        },
+        'roofline': line_roof,
+        'cpu_baseline': cpu,
+        'native_libraries': [os.path.relpath(p, ROOT) for p in _native.loaded_libraries()],
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == '__main__':
+    main()

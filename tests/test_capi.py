@@ -1,0 +1,134 @@
+"""The C ABI library loads, exports what include/vectra_rbf.h declares, and
+validates its arguments on the host.  No kernel is launched here."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from vectra_amd.kernels import _native
+from vectra_amd.kernels import capi
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), 'include', 'vectra_rbf.h')
+
+
+def _declared_functions() -> set[str]:
+    text = open(HEADER, encoding='utf-8').read()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return set(re.findall(r'^\s*(?:const\s+)?\w+\s*\*?\s*(vectra_\w+)\s*\(', text, flags=re.M))
+
+
+def test_header_declares_the_bound_functions():
+    assert _declared_functions() == set(capi.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_native.HIP_LIBRARY)
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_status_strings():
+    assert capi.abi_version() == (1, 0)
+    for status in range(8):
+        assert capi.status_string(status)
+    assert capi.status_string(capi.OK) == 'ok'
+    assert capi.status_string(99) == 'unknown status'
+
+
+def _fake_args(dtype=torch.bfloat16, b=4, h=8, n_q=1, n_k=64, d=32, dv=32, *,
+               out_dtype=None, base=1 << 20, variant='auto', contiguous=True):
+    """Arguments with fake (never dereferenced) device addresses."""
+    a = capi.RbfArgs()
+    a.struct_size = ctypes.sizeof(capi.RbfArgs)
+    a.q, a.k, a.v, a.out, a.scale = base, base + (1 << 16), base + (2 << 16), base + (3 << 16), base + (4 << 16)
+    a.key_bias = None
+    a.in_dtype = capi.DTYPES[dtype]
+    a.out_dtype = capi.DTYPES[out_dtype or dtype]
+    a.scale_dtype = capi.F32
+    a.bias_dtype = capi.F32
+    a.batch, a.heads, a.n_q, a.n_k, a.head_dim, a.value_dim = b, h, n_q, n_k, d, dv
+    if contiguous:
+        a.q_stride = (ctypes.c_int64 * 4)(h * n_q * d, n_q * d, d, 1)
+        a.k_stride = (ctypes.c_int64 * 4)(h * n_k * d, n_k * d, d, 1)
+        a.v_stride = (ctypes.c_int64 * 4)(h * n_k * dv, n_k * dv, dv, 1)
+    else:  # head-transposed views of a [B, N, 3*H*D] projection
+        a.q_stride = (ctypes.c_int64 * 4)(n_q * 3 * h * d, d, 3 * h * d, 1)
+        a.k_stride = (ctypes.c_int64 * 4)(n_k * 3 * h * d, d, 3 * h * d, 1)
+        a.v_stride = (ctypes.c_int64 * 4)(n_k * 3 * h * d, d, 3 * h * d, 1)
+    a.out_stride = (ctypes.c_int64 * 4)(h * n_q * dv, n_q * dv, dv, 1)
+    a.scale_stride_b, a.scale_stride_h = 0, 1
+    a.variant = capi.VARIANTS[variant]
+    return a
+
+
+def test_struct_layout_is_accepted():
+    assert ctypes.sizeof(capi.RbfArgs) == 296
+    assert capi.select_variant(_fake_args()) > 0
+    bad = _fake_args()
+    bad.struct_size -= 8
+    assert capi.select_variant(bad) == -capi.ERR_BAD_STRUCT
+
+
+@pytest.mark.parametrize(
+    'kwargs,variant',
+    [
+        ({}, 'stream'),  # the serving shape
+        ({'dtype': torch.float32, 'd': 16, 'dv': 16, 'n_k': 32}, 'stream'),  # config 1
+        ({'out_dtype': torch.float32}, 'stream'),
+        ({'d': 16, 'dv': 16, 'contiguous': False}, 'stream'),  # model views, 16-B rows
+        ({'d': 24, 'dv': 24}, 'generic'),  # 3 chunks: not a power of two
+        ({'d': 32, 'dv': 16}, 'generic'),  # D != Dv
+        ({'d': 7, 'dv': 7}, 'generic'),
+        ({'base': (1 << 20) + 2}, 'generic'),  # misaligned rows
+    ],
+)
+def test_variant_selection(kwargs, variant):
+    assert capi.VARIANT_NAMES[capi.select_variant(_fake_args(**kwargs))] == variant
+
+
+def test_forcing_a_variant_that_cannot_run_is_an_error():
+    a = _fake_args(d=24, dv=24, variant='stream')
+    assert capi.select_variant(a) == -capi.ERR_BAD_VARIANT
+    assert capi.select_variant(_fake_args(variant='generic')) == capi.VARIANTS['generic']
+
+
+@pytest.mark.parametrize(
+    'field,value,status',
+    [
+        ('in_dtype', 3, capi.ERR_BAD_DTYPE),  # f64 q/k/v
+        ('out_dtype', 9, capi.ERR_BAD_DTYPE),
+        ('scale_dtype', -1, capi.ERR_BAD_DTYPE),
+        ('n_k', -1, capi.ERR_BAD_SHAPE),
+        ('q', None, capi.ERR_NULL_ARGUMENT),
+        ('scale', None, capi.ERR_NULL_ARGUMENT),
+        ('variant', 11, capi.ERR_BAD_VARIANT),
+    ],
+)
+def test_invalid_arguments_are_rejected_before_any_launch(field, value, status):
+    a = _fake_args()
+    setattr(a, field, value)
+    assert capi.select_variant(a) == -status
+    lib = _native.hip_library()
+    assert lib.vectra_rbf_attention_fwd(ctypes.byref(a), None) == status
+
+
+def test_empty_problems_are_a_no_op():
+    lib = _native.hip_library()
+    for field in ('batch', 'heads', 'n_q', 'value_dim'):
+        a = _fake_args()
+        setattr(a, field, 0)
+        a.q = a.k = a.v = a.out = a.scale = None  # never touched
+        assert lib.vectra_rbf_attention_fwd(ctypes.byref(a), None) == capi.OK
+    assert lib.vectra_rbf_attention_fwd(None, None) == capi.ERR_NULL_ARGUMENT
+
+
+def test_squared_norms_validates_on_the_host():
+    lib = _native.hip_library()
+    strides = (ctypes.c_int64 * 4)(0, 0, 0, 1)
+    assert lib.vectra_rbf_squared_norms(None, 7, 1, 1, 1, 1, strides, None, None) == capi.ERR_BAD_DTYPE
+    assert lib.vectra_rbf_squared_norms(None, 0, 1, -1, 1, 1, strides, None, None) == capi.ERR_BAD_SHAPE
+    assert lib.vectra_rbf_squared_norms(None, 0, 0, 1, 1, 1, strides, None, None) == capi.OK
+    assert lib.vectra_rbf_squared_norms(None, 0, 1, 1, 1, 1, strides, None, None) == capi.ERR_NULL_ARGUMENT

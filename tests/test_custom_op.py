@@ -1,0 +1,147 @@
+"""vectra::rbf_attention is a well-formed PyTorch operator (CPU checks).
+
+Restates the reference's kernels/tests/test_custom_op.py:37-82 and the
+operator's error behaviour (spatial_rbf_attention.py:220-236)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rbf as oracle
+from tests import _golden
+from vectra_amd.kernels import custom_ops
+
+
+def _inputs(device='cpu', dtype=torch.float32, bias=True):
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randn(2, 3, 5, 16, generator=gen)
+    k = torch.randn(2, 3, 9, 16, generator=gen)
+    v = torch.randn(2, 3, 9, 8, generator=gen)
+    scale = torch.rand(1, 3, 1, 1, generator=gen) * 0.1 + 0.02
+    key_bias = torch.zeros(2, 1, 1, 9)
+    key_bias[1, ..., 7:] = float('-inf')
+    args = [t.to(device=device, dtype=dtype) for t in (q, k, v)]
+    args += [scale.to(device), key_bias.to(device, dtype) if bias else None]
+    return tuple(args)
+
+
+def test_schema_is_the_reference_schema():
+    schema = str(torch.ops.vectra.rbf_attention.default._schema)
+    assert schema == (
+        'vectra::rbf_attention(Tensor q, Tensor k, Tensor v, Tensor scale, '
+        'Tensor? key_bias=None) -> Tensor'
+    )
+    assert custom_ops.OP_NAME == 'vectra::rbf_attention'
+
+
+@pytest.mark.parametrize('bias', [True, False])
+def test_opcheck(bias):
+    torch.library.opcheck(
+        torch.ops.vectra.rbf_attention.default,
+        _inputs(bias=bias),
+        test_utils=(
+            'test_schema',
+            'test_faketensor',
+            'test_aot_dispatch_static',
+            'test_aot_dispatch_dynamic',
+        ),
+    )
+
+
+def test_operator_matches_the_float64_oracle():
+    args = _inputs()
+    out = torch.ops.vectra.rbf_attention(*args)
+    np.testing.assert_allclose(out.double().numpy(), oracle.expanded_fp64(*args), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize('name', sorted(_golden.cases()))
+def test_cpu_implementation_matches_the_fixtures(name):
+    case = _golden.cases()[name]
+    out = torch.ops.vectra.rbf_attention(case['q'], case['k'], case['v'], case['scale'], case['bias'])
+    assert out.dtype == case['dtype'] and out.is_contiguous()
+    want = case['expected'].numpy()
+    if case['dtype'] == torch.float32:
+        atol = 2e-3 if name == 'far_points' else 1e-5
+        np.testing.assert_allclose(out.double().numpy(), want, rtol=1e-5, atol=atol, equal_nan=True)
+    else:  # one rounding of the fp32 result to the output dtype
+        np.testing.assert_allclose(out.double().numpy(), want, rtol=8e-3, atol=1e-3, equal_nan=True)
+
+
+def test_fake_implementation_reports_the_output_shape():
+    with torch._subclasses.fake_tensor.FakeTensorMode():  # pylint: disable=protected-access
+        q = torch.empty(4, 2, 7, 32, dtype=torch.float16)
+        k = torch.empty(4, 2, 11, 32, dtype=torch.float16)
+        v = torch.empty(4, 2, 11, 24, dtype=torch.float16)
+        out = torch.ops.vectra.rbf_attention(q, k, v, torch.empty(1, 2, 1, 1), None)
+    assert out.shape == (4, 2, 7, 24) and out.dtype == torch.float16
+
+
+def test_strided_head_transposed_views_need_no_copy():
+    gen = torch.Generator().manual_seed(8)
+    projected = torch.randn(4, 65, 3 * 4 * 32, generator=gen)
+    q, k, v = (t.view(4, 65, 4, 32).transpose(1, 2) for t in projected.split(4 * 32, dim=-1))
+    assert not q.is_contiguous()
+    bias = torch.zeros(4, 4, 1, 65)
+    bias[1, 2, 0, 40:] = -math.inf
+    scale = torch.full((1, 4, 1, 1), 0.02)
+    out = torch.ops.vectra.rbf_attention(q, k, v, scale, bias)
+    np.testing.assert_allclose(out.double().numpy(), oracle.expanded_fp64(q, k, v, scale, bias), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize('scale', [torch.tensor(0.1), torch.tensor([[[[0.1]]]], dtype=torch.float64),
+                                   torch.full((2, 3, 1, 1), 0.1, dtype=torch.bfloat16)])
+def test_scale_shapes_and_dtypes(scale):
+    q, k, v, _, bias = _inputs()
+    out = torch.ops.vectra.rbf_attention(q, k, v, scale, bias)
+    np.testing.assert_allclose(out.double().numpy(), oracle.expanded_fp64(q, k, v, scale.float(), bias),
+                               rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize('bias_shape', [(9,), (1, 9), (2, 1, 1, 9), (2, 3, 1, 9), (1, 1, 1, 1)])
+def test_bias_broadcasts(bias_shape):
+    q, k, v, scale, _ = _inputs()
+    gen = torch.Generator().manual_seed(1)
+    bias = torch.randn(*bias_shape, generator=gen)
+    out = torch.ops.vectra.rbf_attention(q, k, v, scale, bias)
+    np.testing.assert_allclose(out.double().numpy(), oracle.expanded_fp64(q, k, v, scale, bias),
+                               rtol=1e-5, atol=1e-6)
+
+
+def test_per_query_bias_is_a_value_error():
+    q, k, v, scale, _ = _inputs()
+    with pytest.raises(ValueError, match='constant across queries'):
+        torch.ops.vectra.rbf_attention(q, k, v, scale, torch.zeros(2, 1, 5, 9))
+
+
+@pytest.mark.parametrize(
+    'mutate',
+    [
+        lambda q, k, v: (q, k.half(), v),  # dtype mismatch
+        lambda q, k, v: (q.double(), k.double(), v.double()),  # unsupported dtype
+        lambda q, k, v: (q, k[..., :8], v),  # head dims differ
+        lambda q, k, v: (q, k, v[:, :, :4]),  # key counts differ
+        lambda q, k, v: (q[0], k, v),  # rank
+    ],
+)
+def test_invalid_inputs_raise(mutate):
+    q, k, v, scale, bias = _inputs()
+    q, k, v = mutate(q, k, v)
+    with pytest.raises(RuntimeError):
+        torch.ops.vectra.rbf_attention(q, k, v, scale, bias)
+
+
+def test_scale_that_does_not_broadcast_raises():
+    q, k, v, _, bias = _inputs()
+    with pytest.raises(RuntimeError):
+        torch.ops.vectra.rbf_attention(q, k, v, torch.ones(5), bias)
+
+
+def test_empty_key_set_gives_zeros_like_eager():
+    q = torch.randn(1, 2, 3, 4)
+    k = torch.empty(1, 2, 0, 4)
+    v = torch.empty(1, 2, 0, 5)
+    out = torch.ops.vectra.rbf_attention(q, k, v, torch.tensor(0.1))
+    assert torch.equal(out, oracle.eager_fp32(q, k, v, torch.tensor(0.1)))
+    assert torch.equal(out, torch.zeros(1, 2, 3, 5))

@@ -1,0 +1,315 @@
+"""Parity of the HIP kernels with the oracle, through the C ABI (GPU).
+
+Gates (from the operator's acceptance targets):
+* bf16 / fp16 inputs: the fp32 output of the kernel within rtol 1e-3 /
+  atol 1e-4 of the eager chain evaluated in fp32 on the same rounded inputs;
+* fp32 inputs: within rtol 1e-5 (atol 1e-6) of the float64 oracle.
+The operator itself returns v.dtype; its output must be exactly the kernel's
+fp32 result rounded once (test_operator_output_is_the_rounded_fp32_result).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rbf as oracle
+from tests import _golden
+from vectra_amd.benchmarks import configs
+from vectra_amd.kernels import _native
+from vectra_amd.kernels import capi
+from vectra_amd.kernels import custom_ops  # noqa: F401  (registers the op)
+
+pytestmark = pytest.mark.gpu
+
+HALF_TOL = {'rtol': 1e-3, 'atol': 1e-4}
+FP32_TOL = {'rtol': 1e-5, 'atol': 1e-6}
+
+
+def _cuda(t):
+    return None if t is None else t.cuda()
+
+
+def _variants(q, k, v, scale, bias):
+    """Every variant the library accepts for these inputs, plus 'auto'."""
+    q, k, v, scale = _cuda(q), _cuda(k), _cuda(v), _cuda(scale)
+    bias = _cuda(bias)
+    scale4, bias4 = capi.broadcast_operands(q, k, scale, bias)
+    out = torch.empty((*q.shape[:-1], v.shape[-1]), device='cuda')
+    found = ['auto']
+    for name in ('generic', 'stream', 'mfma'):
+        if capi.select_variant(capi.make_args(q, k, v, out, scale4, bias4, name)) > 0:
+            found.append(name)
+    return found
+
+
+def run(q, k, v, scale, bias=None, variant='auto', out_dtype=torch.float32):
+    out = capi.forward(_cuda(q), _cuda(k), _cuda(v), _cuda(scale), _cuda(bias),
+                       out_dtype=out_dtype, variant=variant)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def _golden_params():
+    params = []
+    for name, case in sorted(_golden.cases().items()):
+        args = (case['q'], case['k'], case['v'], case['scale'], case['bias'])
+        if torch.cuda.is_available():
+            variants = _variants(*args)
+        else:
+            variants = ['auto']
+        params += [(name, variant) for variant in variants]
+    return params
+
+
+@pytest.mark.parametrize('name,variant', _golden_params())
+def test_golden_fixtures(name, variant):
+    case = _golden.cases()[name]
+    print(f'golden case={name} variant={variant}', flush=True)
+    got = run(case['q'], case['k'], case['v'], case['scale'], case['bias'], variant)
+    want = case['expected'].numpy()
+    if case['dtype'] == torch.float32:
+        tol = {'rtol': 1e-4, 'atol': 1e-4} if name == 'far_points' else FP32_TOL
+    else:
+        tol = HALF_TOL
+    np.testing.assert_allclose(got.double().numpy(), want, equal_nan=True, **tol)
+
+
+# (config, batch subset for the oracle)
+CONFIG_CASES = [
+    (configs.CPU_EAGER, None),
+    (configs.SERVING, None),
+    (configs.SELF_ATTENTION, 48),
+    (configs.SELF_ATTENTION.with_dtype(torch.float32), 48),
+    (configs.SERVING.with_dtype(torch.float16), 128),
+]
+
+
+@pytest.mark.parametrize('config,batch', CONFIG_CASES, ids=lambda c: getattr(c, 'name', str(c)))
+def test_config_parity(config, batch):
+    inputs = configs.make_inputs(config, seed=0, batch=batch)
+    for variant in _variants(*inputs.args()):
+        print(f'config={config.name} batch={batch} variant={variant}', flush=True)
+        got = run(*inputs.args(), variant=variant).double().numpy()
+        if config.dtype == torch.float32:
+            want = oracle.direct_fp64(*inputs.args())
+            np.testing.assert_allclose(got, want, **FP32_TOL)
+        else:
+            want = oracle.eager_fp32(*inputs.args(), batch_chunk=16).double().numpy()
+            np.testing.assert_allclose(got, want, **HALF_TOL)
+
+
+def test_long_key_rows_against_the_expansion():
+    # Config 4's full key axis (4096) for a slice of query rows and planes.
+    config = configs.LONG_KEY
+    gen = torch.Generator().manual_seed(0)
+    q = (0.5 * torch.randn(2, 16, 24, 64, generator=gen)).bfloat16()
+    k = (0.5 * torch.randn(2, 16, 4096, 64, generator=gen)).bfloat16()
+    v = torch.randn(2, 16, 4096, 64, generator=gen).bfloat16()
+    scale = 0.005 + 0.045 * torch.rand(1, 16, 1, 1, generator=gen)
+    assert config.head_dim == 64
+    want = oracle.expanded_fp64(q, k, v, scale)
+    for variant in _variants(q, k, v, scale, None):
+        print(f'long_key slice variant={variant}', flush=True)
+        got = run(q, k, v, scale, None, variant).double().numpy()
+        np.testing.assert_allclose(got, want, **HALF_TOL)
+
+
+def test_operator_output_is_the_rounded_fp32_result():
+    inputs = configs.make_inputs(configs.SERVING, seed=1).to('cuda')
+    out = torch.ops.vectra.rbf_attention(*inputs.args())
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16 and out.is_cuda and out.is_contiguous()
+    fp32 = capi.forward(*inputs.args(), out_dtype=torch.float32)
+    assert torch.equal(out, fp32.to(torch.bfloat16))
+    loaded = _native.loaded_libraries()
+    assert _native.HIP_LIBRARY in loaded and _native.TORCH_LIBRARY in loaded
+
+
+def test_full_serving_size_properties():
+    config = configs.SERVING
+    inputs = configs.make_inputs(config, seed=2).to('cuda')
+    q, k, v, scale, bias = inputs.args()
+    base = capi.forward(q, k, v, scale, bias, out_dtype=torch.float32)
+    # Rows are independent: a sub-batch reproduces its rows bit for bit.
+    part = capi.forward(q[100:300], k[100:300], v[100:300], scale, bias[100:300],
+                        out_dtype=torch.float32)
+    assert torch.equal(part, base[100:300])
+    # Key order does not matter (up to fp32 summation order).
+    perm = torch.randperm(config.n_k, generator=torch.Generator().manual_seed(0)).cuda()
+    permuted = capi.forward(q, k[:, :, perm], v[:, :, perm], scale, bias[..., perm],
+                            out_dtype=torch.float32)
+    torch.testing.assert_close(permuted, base, rtol=1e-5, atol=1e-6)
+    # A constant added to every key's bias changes nothing.
+    shifted = capi.forward(q, k, v, scale, bias.float() + 2.5, out_dtype=torch.float32)
+    torch.testing.assert_close(shifted, base, rtol=1e-5, atol=1e-6)
+    # Outputs are convex combinations of the live values.
+    live = torch.isfinite(bias.float())[:, :, 0, :, None]  # [B,1,Nk,1]
+    vf = v.float()
+    lo = torch.where(live, vf, torch.inf).amin(2, keepdim=True)
+    hi = torch.where(live, vf, -torch.inf).amax(2, keepdim=True)
+    assert bool(((base >= lo - 1e-5) & (base <= hi + 1e-5)).all())
+    # The bf16 operator output is the rounded fp32 one.
+    assert torch.equal(torch.ops.vectra.rbf_attention(q, k, v, scale, bias), base.to(torch.bfloat16))
+
+
+def test_variants_agree_at_full_self_attention_size():
+    inputs = configs.make_inputs(configs.SELF_ATTENTION, seed=3).to('cuda')
+    results = {}
+    for variant in _variants(*inputs.args()):
+        if variant == 'generic':
+            continue  # slow at this size; covered at reduced size above
+        results[variant] = capi.forward(*inputs.args(), out_dtype=torch.float32, variant=variant)
+    ref = results.pop('auto')
+    for variant, out in results.items():
+        torch.testing.assert_close(out, ref, rtol=1e-5, atol=2e-6, msg=variant)
+
+
+# --- Edge shapes and values (kernels/tests/test_edges.py:37-114). ----------
+
+
+def _check(q, k, v, scale, bias=None, tol=None):
+    want = oracle.expanded_fp64(q, k, v, scale, bias)
+    for variant in _variants(q, k, v, scale, bias):
+        got = run(q, k, v, scale, bias, variant).double().numpy()
+        np.testing.assert_allclose(got, want, equal_nan=True, err_msg=variant, **(tol or FP32_TOL))
+
+
+@pytest.mark.parametrize('n_q,n_k', [(1, 1), (1, 65), (17, 3), (63, 65), (65, 63), (129, 1), (130, 200)])
+def test_tails_not_multiple_of_tiles(n_q, n_k):
+    gen = torch.Generator().manual_seed(n_q * 1000 + n_k)
+    q = torch.randn(2, 3, n_q, 32, generator=gen)
+    k = torch.randn(2, 3, n_k, 32, generator=gen)
+    v = torch.randn(2, 3, n_k, 32, generator=gen)
+    _check(q, k, v, torch.tensor(0.02))
+    _check(q.bfloat16(), k.bfloat16(), v.bfloat16(), torch.tensor(0.02), tol=HALF_TOL)
+
+
+@pytest.mark.parametrize('dim,value_dim', [(8, 8), (16, 16), (48, 48), (64, 64), (80, 24), (100, 128),
+                                           (128, 7), (128, 128), (300, 300)])
+def test_head_dims(dim, value_dim):
+    gen = torch.Generator().manual_seed(dim)
+    q = torch.randn(1, 2, 40, dim, generator=gen)
+    k = torch.randn(1, 2, 70, dim, generator=gen)
+    v = torch.randn(1, 2, 70, value_dim, generator=gen)
+    _check(q, k, v, torch.tensor(1.0 / (4.0 * dim)), tol={'rtol': 1e-5, 'atol': 2e-6})
+    _check(q.half(), k.half(), v.half(), torch.tensor(1.0 / (4.0 * dim)), tol=HALF_TOL)
+
+
+def test_all_but_one_key_masked():
+    gen = torch.Generator().manual_seed(5)
+    q = torch.randn(3, 2, 9, 16, generator=gen)
+    k = torch.randn(3, 2, 70, 16, generator=gen)
+    v = torch.randn(3, 2, 70, 16, generator=gen)
+    bias = torch.full((3, 1, 1, 70), -math.inf)
+    bias[..., 0] = 0.0
+    for variant in _variants(q, k, v, torch.tensor(0.05), bias):
+        out = run(q, k, v, torch.tensor(0.05), bias, variant)
+        torch.testing.assert_close(out, v[:, :, :1].expand_as(out), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize('n_k', [20, 64, 130])
+def test_fully_masked_rows_are_nan(n_k):
+    q, k, v = torch.randn(2, 1, 4, 16), torch.randn(2, 1, n_k, 16), torch.randn(2, 1, n_k, 16)
+    bias = torch.zeros(2, 1, 1, n_k)
+    bias[1] = -math.inf
+    for variant in _variants(q, k, v, torch.tensor(0.1), bias):
+        out = run(q, k, v, torch.tensor(0.1), bias, variant)
+        assert torch.isnan(out[1]).all() and torch.isfinite(out[0]).all(), variant
+
+
+def test_far_points_do_not_underflow():
+    gen = torch.Generator().manual_seed(6)
+    q = torch.randn(2, 2, 10, 32, generator=gen) * 20
+    k = torch.randn(2, 2, 50, 32, generator=gen) * 20
+    v = torch.randn(2, 2, 50, 32, generator=gen)
+    _check(q, k, v, torch.tensor(0.1), tol={'rtol': 1e-4, 'atol': 1e-4})
+
+
+@pytest.mark.parametrize('scale', [0.0, -0.01, 3.0])
+def test_degenerate_and_negative_scales(scale):
+    gen = torch.Generator().manual_seed(7)
+    q = torch.randn(1, 2, 12, 16, generator=gen)
+    k = torch.randn(1, 2, 30, 16, generator=gen)
+    v = torch.randn(1, 2, 30, 16, generator=gen)
+    _check(q, k, v, torch.tensor(scale), tol={'rtol': 1e-5, 'atol': 1e-5})
+
+
+def test_head_transposed_views_and_per_head_bias():
+    gen = torch.Generator().manual_seed(8)
+    projected = torch.randn(4, 65, 3 * 4 * 32, generator=gen)
+    for dtype in (torch.float32, torch.bfloat16):
+        proj = projected.to(dtype).cuda()
+        q, k, v = (t.view(4, 65, 4, 32).transpose(1, 2) for t in proj.split(4 * 32, dim=-1))
+        assert not q.is_contiguous()
+        bias = torch.zeros(4, 4, 1, 65)
+        bias[1, 2, 0, 40:] = -math.inf
+        _check(q, k, v, torch.full((1, 4, 1, 1), 0.02), bias,
+               tol=FP32_TOL if dtype == torch.float32 else HALF_TOL)
+
+
+@pytest.mark.parametrize('bias_dtype', [torch.float32, torch.float16, torch.bfloat16, torch.float64])
+@pytest.mark.parametrize('scale_dtype', [torch.float32, torch.bfloat16, torch.float64])
+def test_bias_and_scale_dtypes(bias_dtype, scale_dtype):
+    gen = torch.Generator().manual_seed(9)
+    q, k, v = (torch.randn(2, 3, n, 32, generator=gen) for n in (2, 40, 40))
+    scale = (0.02 + 0.05 * torch.rand(2, 3, 1, 1, generator=gen)).to(scale_dtype)
+    bias = torch.randn(2, 1, 1, 40, generator=gen).to(bias_dtype)
+    bias[0, ..., 30:] = -math.inf
+    _check(q, k, v, scale.float(), bias.double(), tol=FP32_TOL)  # oracle on converted values
+    for variant in _variants(q, k, v, scale, bias):
+        got = run(q, k, v, scale, bias, variant).double().numpy()
+        want = oracle.expanded_fp64(q, k, v, scale.float(), bias.float())
+        np.testing.assert_allclose(got, want, **FP32_TOL)
+
+
+def test_empty_key_set_gives_zeros():
+    q = torch.randn(1, 2, 3, 32)
+    k, v = torch.empty(1, 2, 0, 32), torch.empty(1, 2, 0, 32)
+    for variant in _variants(q, k, v, torch.tensor(0.1), None):
+        assert torch.equal(run(q, k, v, torch.tensor(0.1), None, variant), torch.zeros(1, 2, 3, 32))
+
+
+def test_operator_with_a_cpu_scalar_scale_and_outputs_in_every_dtype():
+    gen = torch.Generator().manual_seed(10)
+    q, k, v = (torch.randn(2, 3, n, 32, generator=gen) for n in (4, 50, 50))
+    want = oracle.expanded_fp64(q, k, v, torch.tensor(0.03))
+    for dtype in (torch.float32, torch.float16, torch.bfloat16):
+        out = torch.ops.vectra.rbf_attention(q.to('cuda', dtype), k.to('cuda', dtype),
+                                             v.to('cuda', dtype), torch.tensor(0.03))
+        assert out.dtype == dtype
+        ref = oracle.expanded_fp64(q.to(dtype), k.to(dtype), v.to(dtype), torch.tensor(0.03))
+        np.testing.assert_allclose(out.double().cpu().numpy(), ref, rtol=1e-2, atol=1e-2)
+    assert want.shape == (2, 3, 4, 32)
+
+
+def test_squared_norms():
+    gen = torch.Generator().manual_seed(12)
+    x = torch.randn(3, 4, 77, 40, generator=gen)
+    for dtype in (torch.float32, torch.float16, torch.bfloat16):
+        xd = x.to('cuda', dtype).transpose(1, 2).contiguous().transpose(1, 2)  # strided
+        got = capi.squared_norms(xd).cpu()
+        want = (x.to(dtype).double() ** 2).sum(-1)
+        np.testing.assert_allclose(got.double().numpy(), want.numpy(), rtol=1e-5, atol=1e-5)
+
+
+def test_graph_replays_match_eager():
+    inputs = configs.make_inputs(configs.SERVING, seed=4, batch=256).to('cuda')
+    eager = torch.ops.vectra.rbf_attention(*inputs.args())
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            torch.ops.vectra.rbf_attention(*inputs.args())
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = torch.ops.vectra.rbf_attention(*inputs.args())
+    for i in range(4):
+        static_out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, eager), f'replay {i}'
+        torch.ops.vectra.rbf_attention(*inputs.args())  # eager work between replays
+        torch.cuda.synchronize()

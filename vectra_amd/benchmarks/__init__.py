@@ -1,0 +1,5 @@
+"""Measurement support: analytic traffic model, BASELINE configs, timing.
+
+Mirrors the reference's kernels/benchmarks (roofline.py, throughput.py) with
+MI355X figures in place of the H100 ones.
+"""

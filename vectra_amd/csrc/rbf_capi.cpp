@@ -1,0 +1,178 @@
+// The C ABI of libvectra_rbf.so: argument validation, kernel selection and
+// launch.  Declared in include/vectra_rbf.h.
+//
+// Replaces the reference's host launch (kernels/vectra_kernels/
+// spatial_rbf_attention.py:177-281) and tile heuristic (tile_configs.py:114-133).
+// Differences by design:
+//  * no device allocation: scale and key_bias are read in place through their
+//    dtype and strides (the reference materialises an fp32 [B*H] scale copy and
+//    an fp32 bias copy, :208-213 and :221);
+//  * the output dtype is a parameter, so a parity harness can read the fp32
+//    result of the same kernel the operator runs in v.dtype.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rbf_common.h"
+#include "rbf_kernels.h"
+#include "vectra_rbf.h"
+
+namespace {
+
+using vectra::Problem;
+
+constexpr int kAbiMajor = 1;
+constexpr int kAbiMinor = 0;
+
+bool is_io_dtype(int32_t d) { return d == VECTRA_F32 || d == VECTRA_F16 || d == VECTRA_BF16; }
+bool is_any_dtype(int32_t d) { return is_io_dtype(d) || d == VECTRA_F64; }
+int elem_size(int32_t d) { return d == VECTRA_F32 ? 4 : (d == VECTRA_F64 ? 8 : 2); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int validate(const vectra_rbf_args* a) {
+  if (a == nullptr) return VECTRA_ERR_NULL_ARGUMENT;
+  if (a->struct_size != static_cast<int64_t>(sizeof(vectra_rbf_args))) return VECTRA_ERR_BAD_STRUCT;
+  if (!is_io_dtype(a->in_dtype) || !is_io_dtype(a->out_dtype) || !is_any_dtype(a->scale_dtype))
+    return VECTRA_ERR_BAD_DTYPE;
+  if (a->key_bias != nullptr && !is_any_dtype(a->bias_dtype)) return VECTRA_ERR_BAD_DTYPE;
+  if (a->batch < 0 || a->heads < 0 || a->n_q < 0 || a->n_k < 0 || a->head_dim < 0 ||
+      a->value_dim < 0)
+    return VECTRA_ERR_BAD_SHAPE;
+  if (a->variant < VECTRA_VARIANT_AUTO || a->variant > VECTRA_VARIANT_MFMA)
+    return VECTRA_ERR_BAD_VARIANT;
+  const int64_t rows = a->batch * a->heads * a->n_q;
+  if (rows == 0 || a->value_dim == 0) return VECTRA_OK;  // nothing to read or write
+  if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->out == nullptr ||
+      a->scale == nullptr)
+    return VECTRA_ERR_NULL_ARGUMENT;
+  // Grids are one wave per query row, four rows per 256-thread block.
+  if ((rows + 3) / 4 > 0x7fffffffLL) return VECTRA_ERR_TOO_LARGE;
+  return VECTRA_OK;
+}
+
+Problem make_problem(const vectra_rbf_args* a) {
+  Problem p{};
+  p.q = a->q;
+  p.k = a->k;
+  p.v = a->v;
+  p.out = a->out;
+  p.scale = a->scale;
+  p.bias = a->key_bias;
+  p.scale_dtype = a->scale_dtype;
+  p.bias_dtype = a->bias_dtype;
+  p.B = a->batch;
+  p.H = a->heads;
+  p.Nq = a->n_q;
+  p.Nk = a->n_k;
+  p.D = a->head_dim;
+  p.Dv = a->value_dim;
+  for (int i = 0; i < 4; ++i) {
+    p.sq[i] = a->q_stride[i];
+    p.sk[i] = a->k_stride[i];
+    p.sv[i] = a->v_stride[i];
+    p.so[i] = a->out_stride[i];
+  }
+  p.ssb = a->scale_stride_b;
+  p.ssh = a->scale_stride_h;
+  p.sbb = a->bias_stride_b;
+  p.sbh = a->bias_stride_h;
+  p.sbn = a->bias_stride_n;
+  p.total_rows = a->batch * a->heads * a->n_q;
+  return p;
+}
+
+// Number of 16-byte chunks per row if the stream kernel can run `a`, else 0.
+int stream_chunks(const vectra_rbf_args* a) {
+  const int in_sz = elem_size(a->in_dtype);
+  const int vec = 16 / in_sz;
+  if (a->head_dim != a->value_dim || a->head_dim == 0 || a->head_dim % vec != 0) return 0;
+  const int64_t chunks = a->head_dim / vec;
+  if (chunks != 1 && chunks != 2 && chunks != 4 && chunks != 8 && chunks != 16) return 0;
+  const int64_t* strides[3] = {a->q_stride, a->k_stride, a->v_stride};
+  const void* ptrs[3] = {a->q, a->k, a->v};
+  for (int t = 0; t < 3; ++t) {
+    if (strides[t][3] != 1 || !aligned16(ptrs[t])) return 0;
+    for (int d = 0; d < 3; ++d)
+      if (strides[t][d] % vec != 0) return 0;
+  }
+  // Output: each lane writes vec contiguous elements of out_dtype (8, 16 or
+  // 32 bytes) with 16-byte stores, or 8-byte stores for an 8-byte chunk.
+  // Strides that are multiples of vec keep every chunk as aligned as the base.
+  const int out_chunk_bytes = vec * elem_size(a->out_dtype);
+  const uintptr_t need = out_chunk_bytes >= 16 ? 16 : 8;
+  if (a->out_stride[3] != 1 || (reinterpret_cast<uintptr_t>(a->out) & (need - 1)) != 0) return 0;
+  for (int d = 0; d < 3; ++d)
+    if (a->out_stride[d] % vec != 0) return 0;
+  return static_cast<int>(chunks);
+}
+
+int select_variant(const vectra_rbf_args* a) {
+  if (a->variant == VECTRA_VARIANT_GENERIC) return VECTRA_VARIANT_GENERIC;
+  if (a->variant == VECTRA_VARIANT_STREAM)
+    return stream_chunks(a) ? VECTRA_VARIANT_STREAM : -VECTRA_ERR_BAD_VARIANT;
+  if (a->variant == VECTRA_VARIANT_MFMA) return -VECTRA_ERR_BAD_VARIANT;
+  return stream_chunks(a) ? VECTRA_VARIANT_STREAM : VECTRA_VARIANT_GENERIC;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vectra_rbf_attention_fwd(const vectra_rbf_args* a, vectra_stream_t stream) {
+  const int status = validate(a);
+  if (status != VECTRA_OK) return status;
+  if (a->batch * a->heads * a->n_q == 0 || a->value_dim == 0) return VECTRA_OK;
+  const int variant = select_variant(a);
+  if (variant < 0) return -variant;
+  Problem p = make_problem(a);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t err = hipErrorInvalidValue;
+  switch (variant) {
+    case VECTRA_VARIANT_STREAM:
+      err = vectra::launch_stream(p, a->in_dtype, a->out_dtype, stream_chunks(a), s);
+      break;
+    default:
+      err = vectra::launch_generic(p, a->in_dtype, a->out_dtype, s);
+      break;
+  }
+  return err == hipSuccess ? VECTRA_OK : VECTRA_ERR_LAUNCH;
+}
+
+int vectra_rbf_squared_norms(const void* x, int32_t dtype, int64_t batch, int64_t heads,
+                             int64_t rows, int64_t cols, const int64_t x_stride[4], float* out,
+                             vectra_stream_t stream) {
+  if (!is_io_dtype(dtype)) return VECTRA_ERR_BAD_DTYPE;
+  if (batch < 0 || heads < 0 || rows < 0 || cols < 0) return VECTRA_ERR_BAD_SHAPE;
+  const int64_t n = batch * heads * rows;
+  if (n == 0) return VECTRA_OK;
+  if (x == nullptr || out == nullptr || x_stride == nullptr) return VECTRA_ERR_NULL_ARGUMENT;
+  if ((n + 255) / 256 > 0x7fffffffLL) return VECTRA_ERR_TOO_LARGE;
+  const hipError_t err = vectra::launch_squared_norms(x, dtype, batch, heads, rows, cols, x_stride,
+                                                      out, reinterpret_cast<hipStream_t>(stream));
+  return err == hipSuccess ? VECTRA_OK : VECTRA_ERR_LAUNCH;
+}
+
+int vectra_rbf_select_variant(const vectra_rbf_args* a) {
+  const int status = validate(a);
+  if (status != VECTRA_OK) return -status;
+  return select_variant(a);
+}
+
+const char* vectra_rbf_status_string(int status) {
+  switch (status) {
+    case VECTRA_OK: return "ok";
+    case VECTRA_ERR_NULL_ARGUMENT: return "a required pointer is NULL";
+    case VECTRA_ERR_BAD_DTYPE: return "unsupported dtype (q/k/v/out: f32, f16 or bf16; scale/bias: f32, f16, bf16 or f64)";
+    case VECTRA_ERR_BAD_SHAPE: return "negative size";
+    case VECTRA_ERR_BAD_STRUCT: return "vectra_rbf_args.struct_size does not match the library";
+    case VECTRA_ERR_TOO_LARGE: return "problem exceeds the kernel grid limits";
+    case VECTRA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case VECTRA_ERR_BAD_VARIANT: return "the requested kernel variant cannot run this problem";
+    default: return "unknown status";
+  }
+}
+
+int vectra_rbf_abi_version(void) { return (kAbiMajor << 16) | kAbiMinor; }
+
+}  // extern "C"

@@ -1,0 +1,22 @@
+// Host-side launchers of the RBF-attention kernels (internal to the library).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vectra {
+
+struct Problem;
+
+// Stream kernel: requires unit element stride in d for q, k, v and out,
+// 16-byte-aligned rows, D == Dv == chunks * (16 / sizeof(input element)),
+// chunks in {1, 2, 4, 8, 16}.
+hipError_t launch_stream(Problem& p, int in_dtype, int out_dtype, int chunks, hipStream_t s);
+
+// Generic kernel: any strides and sizes.
+hipError_t launch_generic(Problem& p, int in_dtype, int out_dtype, hipStream_t s);
+
+hipError_t launch_squared_norms(const void* x, int dtype, int64_t B, int64_t H, int64_t N,
+                                int64_t D, const int64_t* strides, float* out, hipStream_t s);
+
+}  // namespace vectra
