@@ -38,43 +38,75 @@ namespace vectra {
 // load.  V is held the same way (requires Dv == D), so a lane owns the value
 // chunk of exactly the keys whose weights it computed and P.V needs no
 // shuffle until the final reduction.
+//
+// Scheduling: the plane decomposition is wave-uniform (scalar registers);
+// every load of a tile (K, V, the key bias, and for the first tile q and the
+// coefficient) is issued before the first wait, and the next tile's loads
+// are issued before the current tile is reduced.  Rows past Nk are loaded
+// from row Nk-1 (always in bounds) and masked afterwards, so no load sits
+// behind a branch.
 // ------------------------------------------------------------------------
+
+template <typename T, int kPasses, int kRowsPerPass>
+struct StreamTile {
+  uint4 k[kPasses];
+  uint4 v[kPasses];
+  RawScalar bias[kPasses];
+};
+
+template <typename T, int kPasses, int kRowsPerPass>
+__device__ __forceinline__ void load_tile(StreamTile<T, kPasses, kRowsPerPass>& t, const Problem& p,
+                                          const char* k_base, const char* v_base,
+                                          int64_t k_row_bytes, int64_t v_row_bytes,
+                                          int64_t bias_base, int64_t j0, int group) {
+  const int64_t last = p.Nk - 1;
+  int64_t row[kPasses];
+#pragma unroll
+  for (int s = 0; s < kPasses; ++s) {
+    const int64_t j = j0 + s * kRowsPerPass + group;
+    row[s] = j < last ? j : last;
+  }
+#pragma unroll
+  for (int s = 0; s < kPasses; ++s) t.k[s] = load16_stream(k_base + row[s] * k_row_bytes);
+#pragma unroll
+  for (int s = 0; s < kPasses; ++s) t.v[s] = load16_stream(v_base + row[s] * v_row_bytes);
+  if (p.bias != nullptr) {
+#pragma unroll
+    for (int s = 0; s < kPasses; ++s)
+      t.bias[s] = load_raw_scalar(p.bias, bias_base + row[s] * p.sbn, p.bias_dtype);
+  }
+}
+
 template <typename T, typename OutT, int kChunks>
 __global__ __launch_bounds__(256) void rbf_stream_kernel(Problem p) {
   constexpr int kVec = Vec<T>::kN;
   constexpr int kRowsPerPass = kWave / kChunks;
   constexpr int kPasses = kChunks;  // kPasses * kRowsPerPass == 64 keys
+  using Tile = StreamTile<T, kPasses, kRowsPerPass>;
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row_id = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int32_t row_id = static_cast<int32_t>(blockIdx.x) * 4 + wave;
   if (row_id >= p.total_rows) return;  // no barriers below: early exit is safe
 
-  const int64_t i = row_id % p.Nq;
-  const int64_t bh = row_id / p.Nq;
-  const int64_t h = bh % p.H;
-  const int64_t b = bh / p.H;
+  // Wave-uniform decomposition (the host guarantees B*H*Nq < 2^31).
+  const int32_t n_q = static_cast<int32_t>(p.Nq);
+  const int32_t heads = static_cast<int32_t>(p.H);
+  const int32_t bh = n_q == 1 ? row_id : row_id / n_q;
+  const int32_t i = row_id - bh * n_q;
+  const int32_t b = __builtin_amdgcn_readfirstlane(bh / heads);
+  const int32_t h = __builtin_amdgcn_readfirstlane(bh - b * heads);
   const int chunk = lane % kChunks;
   const int group = lane / kChunks;
 
-  const T* q_ptr = static_cast<const T*>(p.q) + b * p.sq[0] + h * p.sq[1] + i * p.sq[2] +
-                   chunk * kVec;
-  const char* k_ptr = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + b * p.sk[0] +
-                                                    h * p.sk[1] + chunk * kVec);
-  const char* v_ptr = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + b * p.sv[0] +
-                                                    h * p.sv[1] + chunk * kVec);
+  const char* k_base = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + b * p.sk[0] +
+                                                     h * p.sk[1] + chunk * kVec);
+  const char* v_base = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + b * p.sv[0] +
+                                                     h * p.sv[1] + chunk * kVec);
   const int64_t k_row_bytes = p.sk[2] * static_cast<int64_t>(sizeof(T));
   const int64_t v_row_bytes = p.sv[2] * static_cast<int64_t>(sizeof(T));
-
-  float qf[kVec];
-  unpack<T>(load16(q_ptr), qf);
-  float q_norm = 0.f;
-#pragma unroll
-  for (int e = 0; e < kVec; ++e) q_norm += qf[e] * qf[e];
-  q_norm = reduce_low<kChunks>(q_norm, OpSum());
-
-  const float neg_scale = -load_any(p.scale, b * p.ssb + h * p.ssh, p.scale_dtype);
-  const bool has_bias = p.bias != nullptr;
   const int64_t bias_base = b * p.sbb + h * p.sbh;
+  const bool has_bias = p.bias != nullptr;
 
   float run_max = -INFINITY;
   float run_sum = 0.f;
@@ -82,78 +114,80 @@ __global__ __launch_bounds__(256) void rbf_stream_kernel(Problem p) {
 #pragma unroll
   for (int e = 0; e < kVec; ++e) acc[e] = 0.f;
 
-  for (int64_t j0 = 0; j0 < p.Nk; j0 += kWave) {
-    uint4 kr[kPasses], vr[kPasses];
-    bool live[kPasses];
-    // Issue every K and V load of the tile before any arithmetic.
+  if (p.Nk > 0) {
+    // First tile, q and the coefficient: all in flight before any wait.
+    Tile cur;
+    load_tile(cur, p, k_base, v_base, k_row_bytes, v_row_bytes, bias_base, 0, group);
+    const uint4 q_raw = load16(static_cast<const T*>(p.q) + b * p.sq[0] + h * p.sq[1] +
+                               i * p.sq[2] + chunk * kVec);
+    const RawScalar scale_raw = load_raw_scalar(p.scale, b * p.ssb + h * p.ssh, p.scale_dtype);
+
+    float qf[kVec];
+    unpack<T>(q_raw, qf);
+    float q_norm = 0.f;
 #pragma unroll
-    for (int s = 0; s < kPasses; ++s) {
-      const int64_t j = j0 + s * kRowsPerPass + group;
-      live[s] = j < p.Nk;
-      kr[s] = live[s] ? load16(k_ptr + j * k_row_bytes) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int s = 0; s < kPasses; ++s) {
-      const int64_t j = j0 + s * kRowsPerPass + group;
-      vr[s] = live[s] ? load16(v_ptr + j * v_row_bytes) : make_uint4(0, 0, 0, 0);
-    }
-    float bias[kPasses];
-    if (has_bias) {
+    for (int e = 0; e < kVec; ++e) q_norm += qf[e] * qf[e];
+    q_norm = reduce_low<kChunks>(q_norm, OpSum());
+    const float neg_scale = -decode_raw_scalar(scale_raw, p.scale_dtype);
+
+    for (int64_t j0 = 0; j0 < p.Nk; j0 += kWave) {
+      Tile next;
+      const bool more = j0 + kWave < p.Nk;
+      if (more)
+        load_tile(next, p, k_base, v_base, k_row_bytes, v_row_bytes, bias_base, j0 + kWave, group);
+
+      float logit[kPasses];
+      bool live[kPasses];
+      float tile_max = -INFINITY;
 #pragma unroll
       for (int s = 0; s < kPasses; ++s) {
-        const int64_t j = j0 + s * kRowsPerPass + group;
-        bias[s] = live[s] ? load_any(p.bias, bias_base + j * p.sbn, p.bias_dtype) : -INFINITY;
+        live[s] = j0 + s * kRowsPerPass + group < p.Nk;
+        float kf[kVec];
+        unpack<T>(cur.k[s], kf);
+        float dot = 0.f, k_norm = 0.f;
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) {
+          dot += qf[e] * kf[e];
+          k_norm += kf[e] * kf[e];
+        }
+        dot = reduce_low<kChunks>(dot, OpSum());
+        k_norm = reduce_low<kChunks>(k_norm, OpSum());
+        const float dist = fmaxf((q_norm + k_norm) - 2.f * dot, 0.f);
+        float x = neg_scale * dist;
+        if (has_bias) x += decode_raw_scalar(cur.bias[s], p.bias_dtype);
+        x = live[s] ? x : -INFINITY;
+        logit[s] = x;
+        tile_max = fmaxf(tile_max, x);
       }
-    }
+      tile_max = reduce_high<kChunks>(tile_max, OpMax());
+      const float new_max = fmaxf(run_max, tile_max);
+      const float safe_max = new_max == -INFINITY ? 0.f : new_max;
+      const float alpha = __builtin_amdgcn_exp2f((run_max - safe_max) * kLog2e);
 
-    float logit[kPasses];
-    float tile_max = -INFINITY;
+      float tile_sum = 0.f;
+      float pv[kVec];
 #pragma unroll
-    for (int s = 0; s < kPasses; ++s) {
-      float kf[kVec];
-      unpack<T>(kr[s], kf);
-      float dot = 0.f, k_norm = 0.f;
+      for (int e = 0; e < kVec; ++e) pv[e] = 0.f;
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) {
-        dot += qf[e] * kf[e];
-        k_norm += kf[e] * kf[e];
+      for (int s = 0; s < kPasses; ++s) {
+        const float w = __builtin_amdgcn_exp2f((logit[s] - safe_max) * kLog2e);
+        tile_sum += w;
+        float vf[kVec];
+        unpack<T>(cur.v[s], vf);
+        // Rows past Nk do not exist: their (clamped) values must not reach
+        // the sum even as 0 * inf.
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) pv[e] += w * (live[s] ? vf[e] : 0.f);
       }
-      dot = reduce_low<kChunks>(dot, OpSum());
-      k_norm = reduce_low<kChunks>(k_norm, OpSum());
-      const float dist = fmaxf((q_norm + k_norm) - 2.f * dot, 0.f);
-      float x = neg_scale * dist;
-      if (has_bias)
-        x += bias[s];
-      else if (!live[s])
-        x = -INFINITY;
-      logit[s] = x;
-      tile_max = fmaxf(tile_max, x);
+      // Each weight is replicated over the kChunks lanes of its key row; sum
+      // over row groups only.
+      tile_sum = reduce_high<kChunks>(tile_sum, OpSum());
+      run_sum = run_sum * alpha + tile_sum;
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) acc[e] = acc[e] * alpha + pv[e];
+      run_max = new_max;
+      if (more) cur = next;
     }
-    tile_max = reduce_high<kChunks>(tile_max, OpMax());
-    const float new_max = fmaxf(run_max, tile_max);
-    const float safe_max = new_max == -INFINITY ? 0.f : new_max;
-    const float alpha = __builtin_amdgcn_exp2f((run_max - safe_max) * kLog2e);
-
-    float tile_sum = 0.f;
-    float pv[kVec];
-#pragma unroll
-    for (int e = 0; e < kVec; ++e) pv[e] = 0.f;
-#pragma unroll
-    for (int s = 0; s < kPasses; ++s) {
-      const float w = __builtin_amdgcn_exp2f((logit[s] - safe_max) * kLog2e);
-      tile_sum += w;
-      float vf[kVec];
-      unpack<T>(vr[s], vf);
-#pragma unroll
-      for (int e = 0; e < kVec; ++e) pv[e] += w * vf[e];
-    }
-    // Each weight is replicated over the kChunks lanes of its key row; sum
-    // over row groups only.
-    tile_sum = reduce_high<kChunks>(tile_sum, OpSum());
-    run_sum = run_sum * alpha + tile_sum;
-#pragma unroll
-    for (int e = 0; e < kVec; ++e) acc[e] = acc[e] * alpha + pv[e];
-    run_max = new_max;
   }
 
 #pragma unroll
@@ -161,14 +195,8 @@ __global__ __launch_bounds__(256) void rbf_stream_kernel(Problem p) {
 
   if (group == 0) {
     float res[kVec];
-    if (p.Nk > 0) {
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) res[e] = acc[e] / run_sum;
-    } else {
-      // softmax over an empty key set contributes nothing (eager gives 0).
-#pragma unroll
-      for (int e = 0; e < kVec; ++e) res[e] = 0.f;
-    }
+    for (int e = 0; e < kVec; ++e) res[e] = p.Nk > 0 ? acc[e] / run_sum : 0.f;
     OutT* o = static_cast<OutT*>(p.out) + b * p.so[0] + h * p.so[1] + i * p.so[2] + chunk * kVec;
     store_chunk<OutT, kVec>(o, res);
   }

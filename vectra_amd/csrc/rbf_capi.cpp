@@ -43,11 +43,12 @@ int validate(const vectra_rbf_args* a) {
     return VECTRA_ERR_BAD_VARIANT;
   const int64_t rows = a->batch * a->heads * a->n_q;
   if (rows == 0 || a->value_dim == 0) return VECTRA_OK;  // nothing to read or write
-  if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->out == nullptr ||
-      a->scale == nullptr)
+  // Buffers with no elements may be NULL (torch gives empty tensors no storage).
+  if (a->out == nullptr || a->scale == nullptr || (a->head_dim > 0 && a->q == nullptr) ||
+      (a->n_k > 0 && a->head_dim > 0 && a->k == nullptr) || (a->n_k > 0 && a->v == nullptr))
     return VECTRA_ERR_NULL_ARGUMENT;
-  // Grids are one wave per query row, four rows per 256-thread block.
-  if ((rows + 3) / 4 > 0x7fffffffLL) return VECTRA_ERR_TOO_LARGE;
+  // Kernels index query rows with 32-bit wave ids.
+  if (rows > 0x7fffffffLL) return VECTRA_ERR_TOO_LARGE;
   return VECTRA_OK;
 }
 
@@ -84,6 +85,9 @@ Problem make_problem(const vectra_rbf_args* a) {
 
 // Number of 16-byte chunks per row if the stream kernel can run `a`, else 0.
 int stream_chunks(const vectra_rbf_args* a) {
+  // The stream kernels decode 2- and 4-byte coefficient and bias elements.
+  if (a->scale_dtype == VECTRA_F64 || (a->key_bias != nullptr && a->bias_dtype == VECTRA_F64))
+    return 0;
   const int in_sz = elem_size(a->in_dtype);
   const int vec = 16 / in_sz;
   if (a->head_dim != a->value_dim || a->head_dim == 0 || a->head_dim % vec != 0) return 0;

@@ -64,6 +64,38 @@ __device__ __forceinline__ float to_float<__bf16>(__bf16 x) { return static_cast
 template <typename T>
 __device__ __forceinline__ T from_float(float x) { return static_cast<T>(x); }
 
+// A 2- or 4-byte float element fetched as the aligned 32-bit word that holds
+// it.  The load has no dtype-dependent control flow, so it can be issued
+// with the tile's other loads and decoded at first use without an early
+// wait.  The aligned word never leaves the element's page.
+struct RawScalar {
+  uint32_t word;
+  uint32_t shift;  // 0 or 16: position of a 2-byte element in the word
+};
+
+__device__ __forceinline__ RawScalar load_raw_scalar(const void* base, int64_t index,
+                                                     int32_t dtype) {
+  // Offsets are formed from `base` itself (not an integer address) so the
+  // access stays a global load rather than a flat one.
+  const int64_t misalign = static_cast<int64_t>(reinterpret_cast<uintptr_t>(base) & 3);
+  const int64_t bytes = index * (dtype == VECTRA_F32 ? 4 : 2) + misalign;
+  RawScalar r;
+  r.word = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(base) + (bytes & ~int64_t{3}) -
+                                              misalign);
+  r.shift = static_cast<uint32_t>(bytes & 2) * 8;
+  return r;
+}
+
+// dtype is F32, F16 or BF16 (F64 operands never reach the stream kernels).
+__device__ __forceinline__ float decode_raw_scalar(RawScalar r, int32_t dtype) {
+  const uint32_t half_bits = (r.word >> r.shift) & 0xffffu;
+  const float as_bf16 = __uint_as_float(half_bits << 16);
+  const float as_f16 = static_cast<float>(
+      __builtin_bit_cast(_Float16, static_cast<uint16_t>(half_bits)));
+  const float as_f32 = __uint_as_float(r.word);
+  return dtype == VECTRA_F32 ? as_f32 : (dtype == VECTRA_BF16 ? as_bf16 : as_f16);
+}
+
 // ---------------------------------------------------------- 16-byte chunks
 
 // Number of elements of T in one 128-bit load.
@@ -102,8 +134,18 @@ __device__ __forceinline__ void unpack<_Float16>(const uint4& r, float* f) {
   for (int i = 0; i < 8; ++i) f[i] = static_cast<float>(h[i]);
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ uint4 load16(const void* p) {
   return *static_cast<const uint4*>(p);
+}
+
+// 128-bit load marked non-temporal: K and V are each read once, so they
+// should not displace reused lines (q, bias) in the caches.  Measured on
+// MI355X, a plain 64 MB read at the serving layout runs 11% faster this way.
+__device__ __forceinline__ uint4 load16_stream(const void* p) {
+  const u32x4 r = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+  return make_uint4(r.x, r.y, r.z, r.w);
 }
 
 // Writes N fp32 values as OutT to a 16-byte-aligned address.
@@ -138,8 +180,21 @@ __device__ __forceinline__ float dpp(float x) {
       __builtin_amdgcn_mov_dpp(__float_as_int(x), kCtrl, 0xf, 0xf, true));
 }
 
-__device__ __forceinline__ float xor_lanes(float x, int mask) {
-  return __shfl_xor(x, mask, kWave);
+// gfx950 lane swaps (VALU, no LDS traffic).  With both operands equal to x,
+// permlane16_swap returns {rows 0,0,2,2 of x; rows 1,1,3,3 of x} (a row is 16
+// lanes) and permlane32_swap returns {lanes 0-31 twice; lanes 32-63 twice}, so
+// op(r[0], r[1]) is the all-reduce over lane bit 16 or bit 32.  The layout
+// was checked on the device.
+template <typename Op>
+__device__ __forceinline__ float allreduce_bit16(float x, Op op) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+template <typename Op>
+__device__ __forceinline__ float allreduce_bit32(float x, Op op) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 struct OpSum {
@@ -174,9 +229,8 @@ __device__ __forceinline__ float reduce_high(float x, Op op) {
   } else if constexpr (kFrom == 8) {
     x = op(x, dpp<0x128>(x));
   }
-  if constexpr (kFrom <= 16) x = op(x, xor_lanes(x, 16));
-  x = op(x, xor_lanes(x, 32));
-  return x;
+  if constexpr (kFrom <= 16) x = allreduce_bit16(x, op);
+  return allreduce_bit32(x, op);
 }
 
 template <typename Op>
