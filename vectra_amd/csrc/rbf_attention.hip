@@ -39,166 +39,266 @@ namespace vectra {
 // chunk of exactly the keys whose weights it computed and P.V needs no
 // shuffle until the final reduction.
 //
-// Scheduling: the plane decomposition is wave-uniform (scalar registers);
-// every load of a tile (K, V, the key bias, and for the first tile q and the
-// coefficient) is issued before the first wait, and the next tile's loads
-// are issued before the current tile is reduced.  Rows past Nk are loaded
-// from row Nk-1 (always in bounds) and masked afterwards, so no load sits
-// behind a branch.
+// Scheduling: the grid is persistent (a fixed number of waves, each taking
+// query rows wave, wave + waves, ...).  A wave always has its next work item
+// (a row and 64-key tile) in flight while it reduces the current one, so the
+// softmax and P.V arithmetic of one row overlaps the HBM stream of the next;
+// a one-shot grid instead leaves every wave waiting for its last bytes until
+// the end of the stream and then serialises all of its arithmetic.  Every
+// load of a work item (K, V, the key bias, and at a row's first tile q and
+// the coefficient) is issued together; rows past Nk are loaded from row
+// Nk - 1 (always in bounds) and masked afterwards, so no load is behind a
+// branch.  Per-lane addresses are 32-bit offsets from wave-uniform bases.
 // ------------------------------------------------------------------------
 
-template <typename T, int kPasses, int kRowsPerPass>
-struct StreamTile {
+template <int kPasses>
+struct StreamSlot {
   uint4 k[kPasses];
   uint4 v[kPasses];
-  RawScalar bias[kPasses];
+  uint32_t bias[kPasses];  // aligned words holding the key biases
+  uint4 q;
+  RawScalar scale;
 };
 
-template <typename T, int kPasses, int kRowsPerPass>
-__device__ __forceinline__ void load_tile(StreamTile<T, kPasses, kRowsPerPass>& t, const Problem& p,
-                                          const char* k_base, const char* v_base,
-                                          int64_t k_row_bytes, int64_t v_row_bytes,
-                                          int64_t bias_base, int64_t j0, int group) {
-  const int64_t last = p.Nk - 1;
-  int64_t row[kPasses];
-#pragma unroll
-  for (int s = 0; s < kPasses; ++s) {
-    const int64_t j = j0 + s * kRowsPerPass + group;
-    row[s] = j < last ? j : last;
-  }
-#pragma unroll
-  for (int s = 0; s < kPasses; ++s) t.k[s] = load16_stream(k_base + row[s] * k_row_bytes);
-#pragma unroll
-  for (int s = 0; s < kPasses; ++s) t.v[s] = load16_stream(v_base + row[s] * v_row_bytes);
-  if (p.bias != nullptr) {
-#pragma unroll
-    for (int s = 0; s < kPasses; ++s)
-      t.bias[s] = load_raw_scalar(p.bias, bias_base + row[s] * p.sbn, p.bias_dtype);
-  }
+struct RowCoords {
+  int32_t b, h, i;
+};
+
+__device__ __forceinline__ RowCoords row_coords(int32_t row, int32_t n_q, int32_t heads) {
+  RowCoords c;
+  const int32_t bh = n_q == 1 ? row : row / n_q;
+  c.i = row - bh * n_q;
+  c.b = bh / heads;
+  c.h = bh - c.b * heads;
+  return c;
 }
 
-template <typename T, typename OutT, int kChunks>
-__global__ __launch_bounds__(256) void rbf_stream_kernel(Problem p) {
+template <typename T, typename OutT, int kChunks, int kRows>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void rbf_stream_kernel(Problem p) {
+  // kRows > 0: the wave takes rows wave * kRows .. + kRows - 1, each one key
+  // tile (Nk <= 64), in a fully unrolled pipeline with no loop and no branch
+  // around a load, so the compiler can wait for exactly the loads each step
+  // needs.  Rows past the end are clamped to the last row: the duplicate
+  // wave recomputes that row and stores the same bytes.
+  // kRows == 0: rows wave, wave + grid_waves, ..., any number of key tiles.
+  constexpr bool kSingleTile = kRows > 0;
   constexpr int kVec = Vec<T>::kN;
   constexpr int kRowsPerPass = kWave / kChunks;
   constexpr int kPasses = kChunks;  // kPasses * kRowsPerPass == 64 keys
-  using Tile = StreamTile<T, kPasses, kRowsPerPass>;
+  using Slot = StreamSlot<kPasses>;
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int32_t row_id = static_cast<int32_t>(blockIdx.x) * 4 + wave;
-  if (row_id >= p.total_rows) return;  // no barriers below: early exit is safe
+  const int32_t wave_id =
+      static_cast<int32_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int32_t total_rows = static_cast<int32_t>(p.total_rows);
+  // No barriers below: early exit is safe.
+  if (wave_id * (kRows > 0 ? kRows : 1) >= total_rows) return;
 
-  // Wave-uniform decomposition (the host guarantees B*H*Nq < 2^31).
+  const int32_t n_waves = p.grid_waves;
   const int32_t n_q = static_cast<int32_t>(p.Nq);
   const int32_t heads = static_cast<int32_t>(p.H);
-  const int32_t bh = n_q == 1 ? row_id : row_id / n_q;
-  const int32_t i = row_id - bh * n_q;
-  const int32_t b = __builtin_amdgcn_readfirstlane(bh / heads);
-  const int32_t h = __builtin_amdgcn_readfirstlane(bh - b * heads);
+  const int32_t n_k = static_cast<int32_t>(p.Nk);
   const int chunk = lane % kChunks;
   const int group = lane / kChunks;
-
-  const char* k_base = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + b * p.sk[0] +
-                                                     h * p.sk[1] + chunk * kVec);
-  const char* v_base = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + b * p.sv[0] +
-                                                     h * p.sv[1] + chunk * kVec);
-  const int64_t k_row_bytes = p.sk[2] * static_cast<int64_t>(sizeof(T));
-  const int64_t v_row_bytes = p.sv[2] * static_cast<int64_t>(sizeof(T));
-  const int64_t bias_base = b * p.sbb + h * p.sbh;
+  const uint32_t chunk_bytes = chunk * 16u;
+  const uint32_t k_row_bytes = static_cast<uint32_t>(p.sk[2]) * sizeof(T);
+  const uint32_t v_row_bytes = static_cast<uint32_t>(p.sv[2]) * sizeof(T);
   const bool has_bias = p.bias != nullptr;
+  const int32_t bias_esize = p.bias_dtype == VECTRA_F32 ? 4 : 2;
+  const uint32_t bias_misalign = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p.bias) & 3);
 
-  float run_max = -INFINITY;
-  float run_sum = 0.f;
-  float acc[kVec];
+  if (n_k == 0) {  // softmax over no keys contributes nothing (eager gives 0)
+    for (int32_t row = wave_id; row < total_rows; row += n_waves) {
+      const RowCoords c = row_coords(row, n_q, heads);
+      float zero[kVec];
 #pragma unroll
-  for (int e = 0; e < kVec; ++e) acc[e] = 0.f;
-
-  if (p.Nk > 0) {
-    // First tile, q and the coefficient: all in flight before any wait.
-    Tile cur;
-    load_tile(cur, p, k_base, v_base, k_row_bytes, v_row_bytes, bias_base, 0, group);
-    const uint4 q_raw = load16(static_cast<const T*>(p.q) + b * p.sq[0] + h * p.sq[1] +
-                               i * p.sq[2] + chunk * kVec);
-    const RawScalar scale_raw = load_raw_scalar(p.scale, b * p.ssb + h * p.ssh, p.scale_dtype);
-
-    float qf[kVec];
-    unpack<T>(q_raw, qf);
-    float q_norm = 0.f;
-#pragma unroll
-    for (int e = 0; e < kVec; ++e) q_norm += qf[e] * qf[e];
-    q_norm = reduce_low<kChunks>(q_norm, OpSum());
-    const float neg_scale = -decode_raw_scalar(scale_raw, p.scale_dtype);
-
-    for (int64_t j0 = 0; j0 < p.Nk; j0 += kWave) {
-      Tile next;
-      const bool more = j0 + kWave < p.Nk;
-      if (more)
-        load_tile(next, p, k_base, v_base, k_row_bytes, v_row_bytes, bias_base, j0 + kWave, group);
-
-      float logit[kPasses];
-      bool live[kPasses];
-      float tile_max = -INFINITY;
-#pragma unroll
-      for (int s = 0; s < kPasses; ++s) {
-        live[s] = j0 + s * kRowsPerPass + group < p.Nk;
-        float kf[kVec];
-        unpack<T>(cur.k[s], kf);
-        float dot = 0.f, k_norm = 0.f;
-#pragma unroll
-        for (int e = 0; e < kVec; ++e) {
-          dot += qf[e] * kf[e];
-          k_norm += kf[e] * kf[e];
-        }
-        dot = reduce_low<kChunks>(dot, OpSum());
-        k_norm = reduce_low<kChunks>(k_norm, OpSum());
-        const float dist = fmaxf((q_norm + k_norm) - 2.f * dot, 0.f);
-        float x = neg_scale * dist;
-        if (has_bias) x += decode_raw_scalar(cur.bias[s], p.bias_dtype);
-        x = live[s] ? x : -INFINITY;
-        logit[s] = x;
-        tile_max = fmaxf(tile_max, x);
-      }
-      tile_max = reduce_high<kChunks>(tile_max, OpMax());
-      const float new_max = fmaxf(run_max, tile_max);
-      const float safe_max = new_max == -INFINITY ? 0.f : new_max;
-      const float alpha = __builtin_amdgcn_exp2f((run_max - safe_max) * kLog2e);
-
-      float tile_sum = 0.f;
-      float pv[kVec];
-#pragma unroll
-      for (int e = 0; e < kVec; ++e) pv[e] = 0.f;
-#pragma unroll
-      for (int s = 0; s < kPasses; ++s) {
-        const float w = __builtin_amdgcn_exp2f((logit[s] - safe_max) * kLog2e);
-        tile_sum += w;
-        float vf[kVec];
-        unpack<T>(cur.v[s], vf);
-        // Rows past Nk do not exist: their (clamped) values must not reach
-        // the sum even as 0 * inf.
-#pragma unroll
-        for (int e = 0; e < kVec; ++e) pv[e] += w * (live[s] ? vf[e] : 0.f);
-      }
-      // Each weight is replicated over the kChunks lanes of its key row; sum
-      // over row groups only.
-      tile_sum = reduce_high<kChunks>(tile_sum, OpSum());
-      run_sum = run_sum * alpha + tile_sum;
-#pragma unroll
-      for (int e = 0; e < kVec; ++e) acc[e] = acc[e] * alpha + pv[e];
-      run_max = new_max;
-      if (more) cur = next;
+      for (int e = 0; e < kVec; ++e) zero[e] = 0.f;
+      if (group == 0)
+        store_chunk<OutT, kVec>(static_cast<OutT*>(p.out) + c.b * p.so[0] + c.h * p.so[1] +
+                                    c.i * p.so[2] + chunk * kVec,
+                                zero);
     }
+    return;
+  }
+  const int32_t tiles = kSingleTile ? 1 : (n_k + kWave - 1) / kWave;
+
+  // Per-lane byte offsets of a tile's keys inside a (b, h) plane.  Those of
+  // tile 0 are the same for every row, so they are computed once: issuing
+  // the next row's loads then only changes wave-uniform base addresses.
+  struct Offsets {
+    uint32_t k[kPasses], v[kPasses], bias[kPasses];
+  };
+  auto tile_offsets = [&](int32_t tile) {
+    Offsets o;
+#pragma unroll
+    for (int s = 0; s < kPasses; ++s) {
+      const int32_t j = tile * kWave + s * kRowsPerPass + group;
+      const uint32_t key = static_cast<uint32_t>(j < n_k - 1 ? j : n_k - 1);
+      o.k[s] = key * k_row_bytes + chunk_bytes;
+      o.v[s] = key * v_row_bytes + chunk_bytes;
+      o.bias[s] = key * static_cast<uint32_t>(p.sbn);
+    }
+    return o;
+  };
+  const Offsets first = tile_offsets(0);
+
+  // Issues every load of work item (row, tile) into `slot`.
+  auto issue = [&](Slot& slot, int32_t row, int32_t tile) {
+    const RowCoords c = row_coords(row, n_q, heads);
+    const char* kp = reinterpret_cast<const char*>(p.k) + (c.b * p.sk[0] + c.h * p.sk[1]) * sizeof(T);
+    const char* vp = reinterpret_cast<const char*>(p.v) + (c.b * p.sv[0] + c.h * p.sv[1]) * sizeof(T);
+    // With one tile per row (Nk <= 64) the offsets are loop invariant.
+    const Offsets o = (kSingleTile || tile == 0) ? first : tile_offsets(tile);
+#pragma unroll
+    for (int s = 0; s < kPasses; ++s) slot.k[s] = load16_stream(kp + o.k[s]);
+#pragma unroll
+    for (int s = 0; s < kPasses; ++s) slot.v[s] = load16_stream(vp + o.v[s]);
+    if (has_bias) {
+      const char* bp = reinterpret_cast<const char*>(p.bias) +
+                       (c.b * p.sbb + c.h * p.sbh) * bias_esize;
+#pragma unroll
+      for (int s = 0; s < kPasses; ++s)
+        slot.bias[s] = load_raw_scalar32(bp, bias_misalign, o.bias[s], p.bias_dtype).word;
+    }
+    if (tile == 0) {
+      const char* qp = reinterpret_cast<const char*>(p.q) +
+                       (c.b * p.sq[0] + c.h * p.sq[1] + c.i * p.sq[2]) * sizeof(T);
+      slot.q = load16(qp + chunk_bytes);
+      slot.scale = load_raw_scalar(p.scale, c.b * p.ssb + c.h * p.ssh, p.scale_dtype);
+    }
+  };
+
+  // Per-row running state.
+  uint4 q_raw = make_uint4(0, 0, 0, 0);
+  float q_norm = 0.f, neg_scale = 0.f, run_max = -INFINITY, run_sum = 0.f;
+  float acc[kVec];
+
+  // Reduces work item (row, tile) held in `slot`.
+  auto consume = [&](const Slot& slot, int32_t row, int32_t tile) {
+    if (tile == 0) {
+      q_raw = slot.q;
+      q_norm = reduce_low<kChunks>(dot_chunk<T>(q_raw, q_raw, 0.f), OpSum());
+      neg_scale = -decode_raw_scalar(slot.scale, p.scale_dtype);
+      run_max = -INFINITY;
+      run_sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) acc[e] = 0.f;
+    }
+    float logit[kPasses];
+    bool live[kPasses];
+    float tile_max = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kPasses; ++s) {
+      const int32_t j = tile * kWave + s * kRowsPerPass + group;
+      live[s] = j < n_k;
+      const float dot = reduce_low<kChunks>(dot_chunk<T>(q_raw, slot.k[s], 0.f), OpSum());
+      const float k_norm = reduce_low<kChunks>(dot_chunk<T>(slot.k[s], slot.k[s], 0.f), OpSum());
+      const float dist = fmaxf((q_norm + k_norm) - 2.f * dot, 0.f);
+      float x = neg_scale * dist;
+      if (has_bias) {
+        // Position of a 2-byte bias inside its word, from the key index
+        // (the same arithmetic as the load).
+        const uint32_t key = static_cast<uint32_t>(j < n_k - 1 ? j : n_k - 1);
+        const uint32_t bytes = key * static_cast<uint32_t>(p.sbn) * bias_esize + bias_misalign;
+        x += decode_raw_scalar(RawScalar{slot.bias[s], (bytes & 2u) * 8u}, p.bias_dtype);
+      }
+      x = live[s] ? x : -INFINITY;
+      logit[s] = x;
+      tile_max = fmaxf(tile_max, x);
+    }
+    tile_max = reduce_high<kChunks>(tile_max, OpMax());
+    const float new_max = fmaxf(run_max, tile_max);
+    const float safe_max = new_max == -INFINITY ? 0.f : new_max;
+    const float alpha = __builtin_amdgcn_exp2f((run_max - safe_max) * kLog2e);
+    float tile_sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[e] *= alpha;
+#pragma unroll
+    for (int s = 0; s < kPasses; ++s) {
+      const float w = __builtin_amdgcn_exp2f((logit[s] - safe_max) * kLog2e);
+      tile_sum += w;
+      float vf[kVec];
+      unpack<T>(slot.v[s], vf);
+      // Rows past Nk do not exist: their (clamped) values must not reach
+      // the sum even as 0 * inf.
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) acc[e] = fmaf(w, live[s] ? vf[e] : 0.f, acc[e]);
+    }
+    // Each weight is replicated over the kChunks lanes of its key row; sum
+    // over row groups only.
+    run_sum = run_sum * alpha + reduce_high<kChunks>(tile_sum, OpSum());
+    run_max = new_max;
+    if (tile == tiles - 1) {
+      float res[kVec];
+      // A row whose keys are all masked has run_sum 0: 0 * inf = NaN, as eager.
+      const float inv = __builtin_amdgcn_rcpf(run_sum);
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) res[e] = reduce_high<kChunks>(acc[e], OpSum()) * inv;
+      if (group == 0) {
+        const RowCoords c = row_coords(row, n_q, heads);
+        store_chunk<OutT, kVec>(static_cast<OutT*>(p.out) + c.b * p.so[0] + c.h * p.so[1] +
+                                    c.i * p.so[2] + chunk * kVec,
+                                res);
+      }
+    }
+  };
+
+  auto advance = [&](int32_t& row, int32_t& tile) {
+    if (kSingleTile) {
+      row += n_waves;
+      return;
+    }
+    if (++tile == tiles) {
+      tile = 0;
+      row += n_waves;
+    }
+  };
+
+  if constexpr (kRows > 0) {
+    Slot slots[2];
+    auto row_at = [&](int r) {
+      const int32_t row = wave_id * kRows + r;
+      return row < total_rows ? row : total_rows - 1;
+    };
+    issue(slots[0], row_at(0), 0);
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      if (r + 1 < kRows) issue(slots[(r + 1) & 1], row_at(r + 1), 0);
+      consume(slots[r & 1], row_at(r), 0);
+    }
+    return;
   }
 
-#pragma unroll
-  for (int e = 0; e < kVec; ++e) acc[e] = reduce_high<kChunks>(acc[e], OpSum());
-
-  if (group == 0) {
-    float res[kVec];
-#pragma unroll
-    for (int e = 0; e < kVec; ++e) res[e] = p.Nk > 0 ? acc[e] / run_sum : 0.f;
-    OutT* o = static_cast<OutT*>(p.out) + b * p.so[0] + h * p.so[1] + i * p.so[2] + chunk * kVec;
-    store_chunk<OutT, kVec>(o, res);
+  // Two slots alternate roles, so the prefetch needs no register copies.
+  // Each branch has its own copy of the reduction: after a join of a path
+  // that issued the prefetch and one that did not, the compiler could only
+  // wait for every outstanding load, the prefetch included.
+  Slot a, b;
+  int32_t row = wave_id, tile = 0;
+  issue(a, row, tile);
+  while (true) {
+    int32_t next_row = row, next_tile = tile;
+    advance(next_row, next_tile);
+    if (next_row < total_rows) {
+      issue(b, next_row, next_tile);
+      consume(a, row, tile);
+    } else {
+      consume(a, row, tile);
+      break;
+    }
+    row = next_row;
+    tile = next_tile;
+    advance(next_row, next_tile);
+    if (next_row < total_rows) {
+      issue(a, next_row, next_tile);
+      consume(b, row, tile);
+    } else {
+      consume(b, row, tile);
+      break;
+    }
+    row = next_row;
+    tile = next_tile;
   }
 }
 
@@ -318,16 +418,43 @@ static hipError_t launch(const void* fn, dim3 grid, dim3 block, Problem& p, hipS
   return hipLaunchKernel(fn, grid, block, args, 0, s);
 }
 
+template <typename T, typename OutT, int kChunks, int kRows>
+static hipError_t launch_stream_k(Problem& p, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((p.grid_waves + 3) / 4));
+  return launch(reinterpret_cast<const void*>(&rbf_stream_kernel<T, OutT, kChunks, kRows>), grid,
+                dim3(256), p, s);
+}
+
+// Rows per wave for one-tile rows: about `budget` waves, at most kMaxRows
+// rows each (the register footprint of two slots bounds it for wide heads).
+template <typename T, typename OutT, int kChunks, int kMaxRows>
+static hipError_t launch_stream_c(Problem& p, hipStream_t s) {
+  const int64_t budget = p.grid_waves;
+  // 16-chunk rows with several key tiles would spill: the host sends them to
+  // the generic kernel instead.
+  if (kChunks == 16 && p.Nk > kWave) return hipErrorInvalidValue;
+  if (kChunks < 16 && p.Nk > kWave) {
+    p.grid_waves = static_cast<int32_t>(p.total_rows < budget ? p.total_rows : budget);
+    return launch_stream_k<T, OutT, kChunks, (kChunks < 16 ? 0 : 1)>(p, s);
+  }
+  const int64_t rows = p.total_rows;
+  int rows_per_wave = rows > 2 * budget ? 4 : (rows > budget ? 2 : 1);
+  if (rows_per_wave > kMaxRows) rows_per_wave = kMaxRows;
+  p.grid_waves = static_cast<int32_t>((rows + rows_per_wave - 1) / rows_per_wave);
+  if (kMaxRows >= 4 && rows_per_wave == 4) return launch_stream_k<T, OutT, kChunks, (kMaxRows >= 4 ? 4 : 1)>(p, s);
+  if (kMaxRows >= 2 && rows_per_wave == 2) return launch_stream_k<T, OutT, kChunks, (kMaxRows >= 2 ? 2 : 1)>(p, s);
+  return launch_stream_k<T, OutT, kChunks, 1>(p, s);
+}
+
+// p.grid_waves holds the persistent wave budget on entry; it is replaced by
+// the number of waves launched.
 template <typename T, typename OutT>
 static hipError_t launch_stream_t(Problem& p, int chunks, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((p.total_rows + 3) / 4));
-  const dim3 block(256);
   switch (chunks) {
-    case 1: return launch(reinterpret_cast<const void*>(&rbf_stream_kernel<T, OutT, 1>), grid, block, p, s);
-    case 2: return launch(reinterpret_cast<const void*>(&rbf_stream_kernel<T, OutT, 2>), grid, block, p, s);
-    case 4: return launch(reinterpret_cast<const void*>(&rbf_stream_kernel<T, OutT, 4>), grid, block, p, s);
-    case 8: return launch(reinterpret_cast<const void*>(&rbf_stream_kernel<T, OutT, 8>), grid, block, p, s);
-    case 16: return launch(reinterpret_cast<const void*>(&rbf_stream_kernel<T, OutT, 16>), grid, block, p, s);
+    case 2: return launch_stream_c<T, OutT, 2, 4>(p, s);
+    case 4: return launch_stream_c<T, OutT, 4, 4>(p, s);
+    case 8: return launch_stream_c<T, OutT, 8, 4>(p, s);
+    case 16: return launch_stream_c<T, OutT, 16, 1>(p, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -356,18 +483,22 @@ static hipError_t by_dtype(int in_dt, int out_dt, A&&... a) {
 }
 
 template <typename T, typename OutT>
-struct StreamLauncher {
-  static hipError_t run(Problem& p, int chunks, hipStream_t s) {
-    return launch_stream_t<T, OutT>(p, chunks, s);
-  }
-};
-template <typename T, typename OutT>
 struct GenericLauncher {
   static hipError_t run(Problem& p, hipStream_t s) { return launch_generic_t<T, OutT>(p, s); }
 };
 
 hipError_t launch_stream(Problem& p, int in_dt, int out_dt, int chunks, hipStream_t s) {
-  return by_dtype<StreamLauncher>(in_dt, out_dt, p, chunks, s);
+  // Output in the input dtype (the operator) or fp32 (parity harnesses).
+  switch (in_dt) {
+    case VECTRA_BF16:
+      return out_dt == VECTRA_F32 ? launch_stream_t<__bf16, float>(p, chunks, s)
+                                  : launch_stream_t<__bf16, __bf16>(p, chunks, s);
+    case VECTRA_F16:
+      return out_dt == VECTRA_F32 ? launch_stream_t<_Float16, float>(p, chunks, s)
+                                  : launch_stream_t<_Float16, _Float16>(p, chunks, s);
+    default:
+      return launch_stream_t<float, float>(p, chunks, s);
+  }
 }
 
 hipError_t launch_generic(Problem& p, int in_dt, int out_dt, hipStream_t s) {

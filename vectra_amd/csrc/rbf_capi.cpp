@@ -12,6 +12,9 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
+
+#include <atomic>
 
 #include "rbf_common.h"
 #include "rbf_kernels.h"
@@ -29,6 +32,34 @@ bool is_any_dtype(int32_t d) { return is_io_dtype(d) || d == VECTRA_F64; }
 int elem_size(int32_t d) { return d == VECTRA_F32 ? 4 : (d == VECTRA_F64 ? 8 : 2); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Compute units of the current device.  Cached per device: a device property
+// never changes, so the cache is the only state the library keeps.
+int device_compute_units() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int cus = cache[dev].load(std::memory_order_relaxed);
+  if (cus > 0) return cus;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+// Resident waves per CU for the persistent stream kernel: 8 (2 per SIMD, the
+// occupancy its register budget allows) by default;
+// VECTRA_STREAM_WAVES_PER_CU (1..32) overrides it for tuning sweeps.
+int stream_waves_per_cu() {
+  static const int value = [] {
+    const char* env = getenv("VECTRA_STREAM_WAVES_PER_CU");
+    const int v = env ? atoi(env) : 0;
+    return (v >= 1 && v <= 32) ? v : 8;
+  }();
+  return value;
+}
 
 int validate(const vectra_rbf_args* a) {
   if (a == nullptr) return VECTRA_ERR_NULL_ARGUMENT;
@@ -85,6 +116,8 @@ Problem make_problem(const vectra_rbf_args* a) {
 
 // Number of 16-byte chunks per row if the stream kernel can run `a`, else 0.
 int stream_chunks(const vectra_rbf_args* a) {
+  // Stream kernels write the input dtype or fp32.
+  if (a->out_dtype != a->in_dtype && a->out_dtype != VECTRA_F32) return 0;
   // The stream kernels decode 2- and 4-byte coefficient and bias elements.
   if (a->scale_dtype == VECTRA_F64 || (a->key_bias != nullptr && a->bias_dtype == VECTRA_F64))
     return 0;
@@ -92,7 +125,17 @@ int stream_chunks(const vectra_rbf_args* a) {
   const int vec = 16 / in_sz;
   if (a->head_dim != a->value_dim || a->head_dim == 0 || a->head_dim % vec != 0) return 0;
   const int64_t chunks = a->head_dim / vec;
-  if (chunks != 1 && chunks != 2 && chunks != 4 && chunks != 8 && chunks != 16) return 0;
+  if (chunks != 2 && chunks != 4 && chunks != 8 && chunks != 16) return 0;
+  // 16-chunk rows run one key tile per row only (more would spill registers).
+  if (chunks == 16 && a->n_k > 64) return 0;
+  // Per-lane key offsets inside a (b, h) plane are 32-bit.
+  const int64_t limit = int64_t{1} << 31;
+  const int64_t last_key = a->n_k > 0 ? a->n_k - 1 : 0;
+  if (last_key * a->k_stride[2] * in_sz + 16 * chunks >= limit ||
+      last_key * a->v_stride[2] * in_sz + 16 * chunks >= limit)
+    return 0;
+  if (a->key_bias != nullptr && last_key * a->bias_stride_n * elem_size(a->bias_dtype) + 4 >= limit)
+    return 0;
   const int64_t* strides[3] = {a->q_stride, a->k_stride, a->v_stride};
   const void* ptrs[3] = {a->q, a->k, a->v};
   for (int t = 0; t < 3; ++t) {
@@ -130,6 +173,8 @@ int vectra_rbf_attention_fwd(const vectra_rbf_args* a, vectra_stream_t stream) {
   const int variant = select_variant(a);
   if (variant < 0) return -variant;
   Problem p = make_problem(a);
+  // Wave budget for the persistent stream kernel (it sizes its own grid).
+  p.grid_waves = device_compute_units() * stream_waves_per_cu();
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t err = hipErrorInvalidValue;
   switch (variant) {

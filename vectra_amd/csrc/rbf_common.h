@@ -28,6 +28,7 @@ struct Problem {
   int64_t ssb, ssh;
   int64_t sbb, sbh, sbn;
   int64_t total_rows;  // B * H * Nq
+  int32_t grid_waves;  // waves launched by persistent kernels (<= total_rows)
 };
 
 // ---------------------------------------------------------------- scalars
@@ -83,6 +84,18 @@ __device__ __forceinline__ RawScalar load_raw_scalar(const void* base, int64_t i
   r.word = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(base) + (bytes & ~int64_t{3}) -
                                               misalign);
   r.shift = static_cast<uint32_t>(bytes & 2) * 8;
+  return r;
+}
+
+// Same, for an element at a 32-bit element offset from a (wave-uniform) base:
+// the address becomes base + 32-bit lane offset, which the global_load
+// instruction encodes directly.
+__device__ __forceinline__ RawScalar load_raw_scalar32(const char* base, uint32_t misalign,
+                                                       uint32_t elem_offset, int32_t dtype) {
+  const uint32_t bytes = elem_offset * (dtype == VECTRA_F32 ? 4u : 2u) + misalign;
+  RawScalar r;
+  r.word = *reinterpret_cast<const uint32_t*>(base + (bytes & ~3u));
+  r.shift = (bytes & 2u) * 8u;
   return r;
 }
 
@@ -146,6 +159,43 @@ __device__ __forceinline__ uint4 load16(const void* p) {
 __device__ __forceinline__ uint4 load16_stream(const void* p) {
   const u32x4 r = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
   return make_uint4(r.x, r.y, r.z, r.w);
+}
+
+// Dot product of two 128-bit chunks in fp32: v_dot2 on packed bf16 / fp16
+// pairs (products of 16-bit floats are exact in fp32), FMAs for fp32.
+template <typename T>
+__device__ __forceinline__ float dot_chunk(const uint4& a, const uint4& b, float acc);
+
+template <>
+__device__ __forceinline__ float dot_chunk<__bf16>(const uint4& a, const uint4& b, float acc) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const uint32_t x[4] = {a.x, a.y, a.z, a.w};
+  const uint32_t y[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x[i]),
+                                          __builtin_bit_cast(bf16x2, y[i]), acc, false);
+  return acc;
+}
+
+template <>
+__device__ __forceinline__ float dot_chunk<_Float16>(const uint4& a, const uint4& b, float acc) {
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  const uint32_t x[4] = {a.x, a.y, a.z, a.w};
+  const uint32_t y[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x[i]), __builtin_bit_cast(f16x2, y[i]),
+                                 acc, false);
+  return acc;
+}
+
+template <>
+__device__ __forceinline__ float dot_chunk<float>(const uint4& a, const uint4& b, float acc) {
+  acc = fmaf(__uint_as_float(a.x), __uint_as_float(b.x), acc);
+  acc = fmaf(__uint_as_float(a.y), __uint_as_float(b.y), acc);
+  acc = fmaf(__uint_as_float(a.z), __uint_as_float(b.z), acc);
+  return fmaf(__uint_as_float(a.w), __uint_as_float(b.w), acc);
 }
 
 // Writes N fp32 values as OutT to a 16-byte-aligned address.

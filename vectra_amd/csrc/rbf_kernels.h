@@ -10,7 +10,7 @@ struct Problem;
 
 // Stream kernel: requires unit element stride in d for q, k, v and out,
 // 16-byte-aligned rows, D == Dv == chunks * (16 / sizeof(input element)),
-// chunks in {1, 2, 4, 8, 16}.
+// chunks in {2, 4, 8, 16}.
 hipError_t launch_stream(Problem& p, int in_dtype, int out_dtype, int chunks, hipStream_t s);
 
 // Generic kernel: any strides and sizes.
