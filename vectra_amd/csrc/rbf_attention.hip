@@ -51,6 +51,48 @@ namespace vectra {
 // branch.  Per-lane addresses are 32-bit offsets from wave-uniform bases.
 // ------------------------------------------------------------------------
 
+// Sums kVec accumulators per lane over the row-group lane bits (kChunks ..
+// 32) of the stream layout.  Lane bits 32 and 16 use butterfly steps: a
+// permlane swap of the value pair (a_i, a_{i+n/2}) hands each half of the
+// wave the partner's copy of the half it keeps, so one swap and one add
+// halve the values per lane.  The remaining row-group bits (below 16) are
+// all-reduced with DPP.  On return res[0 .. kVec/4) are the finished sums of
+// elements first_e .. first_e + kVec/4 of the lane's chunk.
+template <int kChunks, int kVec>
+__device__ __forceinline__ void reduce_rows_butterfly(const float* acc, float* res, int& first_e) {
+  const int lane = threadIdx.x & (kWave - 1);
+  constexpr int kHalf = kVec / 2, kQuarter = kVec / 4;
+  float half[kHalf];
+#pragma unroll
+  for (int i = 0; i < kHalf; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]),
+                                                    __float_as_uint(acc[i + kHalf]), false, false);
+    half[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // lanes < 32: a_i, else a_{i+n/2}
+  }
+#pragma unroll
+  for (int i = 0; i < kQuarter; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(half[i]),
+                                                    __float_as_uint(half[i + kQuarter]), false, false);
+    res[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  first_e = ((lane & 32) ? kHalf : 0) + ((lane & 16) ? kQuarter : 0);
+  if constexpr (kChunks < 16) {
+#pragma unroll
+    for (int i = 0; i < kQuarter; ++i) {
+      float x = res[i];
+      if constexpr (kChunks <= 1) x += dpp<0xB1>(x);
+      if constexpr (kChunks <= 2) x += dpp<0x4E>(x);
+      if constexpr (kChunks <= 4) {
+        x += dpp<0x124>(x);
+        x += dpp<0x128>(x);
+      } else {
+        x += dpp<0x128>(x);
+      }
+      res[i] = x;
+    }
+  }
+}
+
 template <int kPasses>
 struct StreamSlot {
   uint4 k[kPasses];
@@ -64,12 +106,12 @@ struct RowCoords {
   int32_t b, h, i;
 };
 
-__device__ __forceinline__ RowCoords row_coords(int32_t row, int32_t n_q, int32_t heads) {
+__device__ __forceinline__ RowCoords row_coords(int32_t row, const Problem& p) {
   RowCoords c;
-  const int32_t bh = n_q == 1 ? row : row / n_q;
-  c.i = row - bh * n_q;
-  c.b = bh / heads;
-  c.h = bh - c.b * heads;
+  const int32_t bh = static_cast<int32_t>(fast_div(row, p.nq_mul, p.nq_shift));
+  c.i = row - bh * static_cast<int32_t>(p.Nq);
+  c.b = static_cast<int32_t>(fast_div(bh, p.h_mul, p.h_shift));
+  c.h = bh - c.b * static_cast<int32_t>(p.H);
   return c;
 }
 
@@ -96,8 +138,6 @@ void rbf_stream_kernel(Problem p) {
   if (wave_id * (kRows > 0 ? kRows : 1) >= total_rows) return;
 
   const int32_t n_waves = p.grid_waves;
-  const int32_t n_q = static_cast<int32_t>(p.Nq);
-  const int32_t heads = static_cast<int32_t>(p.H);
   const int32_t n_k = static_cast<int32_t>(p.Nk);
   const int chunk = lane % kChunks;
   const int group = lane / kChunks;
@@ -110,7 +150,7 @@ void rbf_stream_kernel(Problem p) {
 
   if (n_k == 0) {  // softmax over no keys contributes nothing (eager gives 0)
     for (int32_t row = wave_id; row < total_rows; row += n_waves) {
-      const RowCoords c = row_coords(row, n_q, heads);
+      const RowCoords c = row_coords(row, p);
       float zero[kVec];
 #pragma unroll
       for (int e = 0; e < kVec; ++e) zero[e] = 0.f;
@@ -145,7 +185,7 @@ void rbf_stream_kernel(Problem p) {
 
   // Issues every load of work item (row, tile) into `slot`.
   auto issue = [&](Slot& slot, int32_t row, int32_t tile) {
-    const RowCoords c = row_coords(row, n_q, heads);
+    const RowCoords c = row_coords(row, p);
     const char* kp = reinterpret_cast<const char*>(p.k) + (c.b * p.sk[0] + c.h * p.sk[1]) * sizeof(T);
     const char* vp = reinterpret_cast<const char*>(p.v) + (c.b * p.sv[0] + c.h * p.sv[1]) * sizeof(T);
     // With one tile per row (Nk <= 64) the offsets are loop invariant.
@@ -214,31 +254,40 @@ void rbf_stream_kernel(Problem p) {
     float tile_sum = 0.f;
 #pragma unroll
     for (int e = 0; e < kVec; ++e) acc[e] *= alpha;
+    // Rows past Nk do not exist: their (clamped) values must not reach the
+    // sum even as 0 * inf, so a tile with such rows zeroes them.
+    const bool ragged = (tile + 1) * kWave > n_k;
 #pragma unroll
     for (int s = 0; s < kPasses; ++s) {
       const float w = __builtin_amdgcn_exp2f((logit[s] - safe_max) * kLog2e);
       tile_sum += w;
+      uint4 vr = slot.v[s];
+      if (ragged && !live[s]) vr = make_uint4(0, 0, 0, 0);
       float vf[kVec];
-      unpack<T>(slot.v[s], vf);
-      // Rows past Nk do not exist: their (clamped) values must not reach
-      // the sum even as 0 * inf.
+      unpack<T>(vr, vf);
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) acc[e] = fmaf(w, live[s] ? vf[e] : 0.f, acc[e]);
+      for (int e = 0; e < kVec; ++e) acc[e] = fmaf(w, vf[e], acc[e]);
     }
     // Each weight is replicated over the kChunks lanes of its key row; sum
     // over row groups only.
     run_sum = run_sum * alpha + reduce_high<kChunks>(tile_sum, OpSum());
     run_max = new_max;
     if (tile == tiles - 1) {
-      float res[kVec];
+      // Sum the accumulators over row groups; lane `lane` ends with
+      // kVec / 4 finished values of its chunk, starting at element `first_e`.
+      constexpr int kOut = kVec / 4;
+      float res[kOut];
+      int first_e;
+      reduce_rows_butterfly<kChunks, kVec>(acc, res, first_e);
       // A row whose keys are all masked has run_sum 0: 0 * inf = NaN, as eager.
       const float inv = __builtin_amdgcn_rcpf(run_sum);
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) res[e] = reduce_high<kChunks>(acc[e], OpSum()) * inv;
-      if (group == 0) {
-        const RowCoords c = row_coords(row, n_q, heads);
-        store_chunk<OutT, kVec>(static_cast<OutT*>(p.out) + c.b * p.so[0] + c.h * p.so[1] +
-                                    c.i * p.so[2] + chunk * kVec,
+      for (int e = 0; e < kOut; ++e) res[e] *= inv;
+      // Row groups below lane bit 16 hold copies; one of them stores.
+      if ((lane & (16 - kChunks)) == 0) {
+        const RowCoords c = row_coords(row, p);
+        store_small<OutT, kOut>(static_cast<OutT*>(p.out) + c.b * p.so[0] + c.h * p.so[1] +
+                                    c.i * p.so[2] + chunk * kVec + first_e,
                                 res);
       }
     }
@@ -430,12 +479,12 @@ static hipError_t launch_stream_k(Problem& p, hipStream_t s) {
 template <typename T, typename OutT, int kChunks, int kMaxRows>
 static hipError_t launch_stream_c(Problem& p, hipStream_t s) {
   const int64_t budget = p.grid_waves;
-  // 16-chunk rows with several key tiles would spill: the host sends them to
-  // the generic kernel instead.
-  if (kChunks == 16 && p.Nk > kWave) return hipErrorInvalidValue;
-  if (kChunks < 16 && p.Nk > kWave) {
+  // Rows of 8 or 16 chunks with several key tiles would spill registers in
+  // the looping variant: the host sends them to another kernel instead.
+  if (kChunks >= 8 && p.Nk > kWave) return hipErrorInvalidValue;
+  if (kChunks < 8 && p.Nk > kWave) {
     p.grid_waves = static_cast<int32_t>(p.total_rows < budget ? p.total_rows : budget);
-    return launch_stream_k<T, OutT, kChunks, (kChunks < 16 ? 0 : 1)>(p, s);
+    return launch_stream_k<T, OutT, kChunks, (kChunks < 8 ? 0 : 1)>(p, s);
   }
   const int64_t rows = p.total_rows;
   int rows_per_wave = rows > 2 * budget ? 4 : (rows > budget ? 2 : 1);

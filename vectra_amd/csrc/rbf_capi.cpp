@@ -49,14 +49,15 @@ int device_compute_units() {
   return cus;
 }
 
-// Resident waves per CU for the persistent stream kernel: 8 (2 per SIMD, the
-// occupancy its register budget allows) by default;
-// VECTRA_STREAM_WAVES_PER_CU (1..32) overrides it for tuning sweeps.
+// Waves per CU the stream kernel is sized for: 32 (8 per SIMD) by default,
+// which at the serving shape gives one row per wave with every wave resident
+// at once (measured fastest on MI355X); VECTRA_STREAM_WAVES_PER_CU (1..32)
+// overrides it for tuning sweeps.
 int stream_waves_per_cu() {
   static const int value = [] {
     const char* env = getenv("VECTRA_STREAM_WAVES_PER_CU");
     const int v = env ? atoi(env) : 0;
-    return (v >= 1 && v <= 32) ? v : 8;
+    return (v >= 1 && v <= 32) ? v : 32;
   }();
   return value;
 }
@@ -81,6 +82,20 @@ int validate(const vectra_rbf_args* a) {
   // Kernels index query rows with 32-bit wave ids.
   if (rows > 0x7fffffffLL) return VECTRA_ERR_TOO_LARGE;
   return VECTRA_OK;
+}
+
+// Multiplier and shift for vectra::fast_div (division of 31-bit values by d).
+void make_fast_div(int64_t d, uint32_t* mul, uint32_t* shift) {
+  uint32_t l = 0;
+  while ((int64_t{1} << l) < d) ++l;  // l = ceil(log2 d)
+  if ((int64_t{1} << l) == d) {
+    *mul = 0;
+    *shift = l;
+    return;
+  }
+  *mul = static_cast<uint32_t>(((uint64_t{1} << (31 + l)) + static_cast<uint64_t>(d) - 1) /
+                               static_cast<uint64_t>(d));
+  *shift = l - 1;
 }
 
 Problem make_problem(const vectra_rbf_args* a) {
@@ -111,6 +126,8 @@ Problem make_problem(const vectra_rbf_args* a) {
   p.sbh = a->bias_stride_h;
   p.sbn = a->bias_stride_n;
   p.total_rows = a->batch * a->heads * a->n_q;
+  make_fast_div(a->n_q > 0 ? a->n_q : 1, &p.nq_mul, &p.nq_shift);
+  make_fast_div(a->heads > 0 ? a->heads : 1, &p.h_mul, &p.h_shift);
   return p;
 }
 
@@ -126,8 +143,9 @@ int stream_chunks(const vectra_rbf_args* a) {
   if (a->head_dim != a->value_dim || a->head_dim == 0 || a->head_dim % vec != 0) return 0;
   const int64_t chunks = a->head_dim / vec;
   if (chunks != 2 && chunks != 4 && chunks != 8 && chunks != 16) return 0;
-  // 16-chunk rows run one key tile per row only (more would spill registers).
-  if (chunks == 16 && a->n_k > 64) return 0;
+  // 8- and 16-chunk rows run one key tile per row only (more would spill
+  // registers in the looping variant).
+  if (chunks >= 8 && a->n_k > 64) return 0;
   // Per-lane key offsets inside a (b, h) plane are 32-bit.
   const int64_t limit = int64_t{1} << 31;
   const int64_t last_key = a->n_k > 0 ? a->n_k - 1 : 0;

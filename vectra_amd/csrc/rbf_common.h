@@ -29,7 +29,18 @@ struct Problem {
   int64_t sbb, sbh, sbn;
   int64_t total_rows;  // B * H * Nq
   int32_t grid_waves;  // waves launched by persistent kernels (<= total_rows)
+  uint32_t nq_mul, nq_shift;  // FastDiv of Nq (see fast_div)
+  uint32_t h_mul, h_shift;    // FastDiv of H
 };
+
+// floor(n / d) for 0 <= n < 2^31 from a multiplier and shift made on the host
+// (make_fast_div): mul == 0 means d is a power of two, else
+// mul = ceil(2^(31+l) / d) with l = ceil(log2 d) and shift = l - 1.  Then
+// n * mul / 2^(31+l) = n/d + err with 0 <= err < n / 2^(31+l) < 1/d, so the
+// floor is exact; mul < 2^32 because d > 2^(l-1).
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t mul, uint32_t shift) {
+  return mul ? (__umulhi(n, mul) >> shift) : (n >> shift);
+}
 
 // ---------------------------------------------------------------- scalars
 
@@ -214,6 +225,22 @@ __device__ __forceinline__ void store_chunk(OutT* dst, const float* f) {
 #pragma unroll
     for (int i = 0; i < kBytes / 8; ++i)
       reinterpret_cast<uint2*>(dst)[i] = reinterpret_cast<const uint2*>(tmp)[i];
+  }
+}
+
+// Writes N (1 or 2) fp32 values as OutT (N * sizeof(OutT)-aligned address).
+template <typename OutT, int N>
+__device__ __forceinline__ void store_small(OutT* dst, const float* f) {
+  if constexpr (N == 1) {
+    dst[0] = from_float<OutT>(f[0]);
+  } else {
+    static_assert(N == 2, "one or two values");
+    if constexpr (sizeof(OutT) == 4) {
+      *reinterpret_cast<float2*>(dst) = make_float2(f[0], f[1]);
+    } else {
+      OutT pair[2] = {from_float<OutT>(f[0]), from_float<OutT>(f[1])};
+      *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(pair);
+    }
   }
 }
 
