@@ -210,8 +210,18 @@ def main():
         line_roof = {'bound': 'hbm', 'achieved': achieved,
                      'peak': roofline.MI355X.hbm_bytes_per_s / 1e9, 'unit': 'GB/s'}
     line_roof['frac'] = line_roof['achieved'] / line_roof['peak']
-    line_roof['traffic'] = None
     line_roof['kernel'] = KERNEL_NAMES.get(variant, variant)
+    line_roof['traffic'] = None
+    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    # runs of this workload (profiles/traffic_<config>.json, made by
+    # vectra_amd.benchmarks.rocprof_summary), if they measured this kernel.
+    traffic_path = os.path.join(ROOT, 'profiles', f'traffic_{config.name}.json')
+    if os.path.exists(traffic_path):
+        with open(traffic_path, encoding='utf-8') as f:
+            measured = json.load(f)
+        if measured.get('kernel') == line_roof['kernel']:
+            line_roof['traffic'] = measured['traffic_bytes']
+            line_roof['traffic_source'] = os.path.relpath(traffic_path, ROOT)
     line_roof['algorithmic_bytes'] = fused
 
     result = {
