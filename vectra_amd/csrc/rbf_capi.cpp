@@ -172,11 +172,19 @@ int stream_chunks(const vectra_rbf_args* a) {
   return static_cast<int>(chunks);
 }
 
+// Query tiles of this many rows or more go to the MFMA kernel.
+constexpr int64_t kMfmaMinQueries = 16;
+
 int select_variant(const vectra_rbf_args* a) {
-  if (a->variant == VECTRA_VARIANT_GENERIC) return VECTRA_VARIANT_GENERIC;
-  if (a->variant == VECTRA_VARIANT_STREAM)
-    return stream_chunks(a) ? VECTRA_VARIANT_STREAM : -VECTRA_ERR_BAD_VARIANT;
-  if (a->variant == VECTRA_VARIANT_MFMA) return -VECTRA_ERR_BAD_VARIANT;
+  const Problem p = make_problem(a);
+  const bool mfma = vectra::mfma_supports(p, a->in_dtype, a->out_dtype);
+  switch (a->variant) {
+    case VECTRA_VARIANT_GENERIC: return VECTRA_VARIANT_GENERIC;
+    case VECTRA_VARIANT_STREAM: return stream_chunks(a) ? VECTRA_VARIANT_STREAM : -VECTRA_ERR_BAD_VARIANT;
+    case VECTRA_VARIANT_MFMA: return mfma ? VECTRA_VARIANT_MFMA : -VECTRA_ERR_BAD_VARIANT;
+    default: break;
+  }
+  if (mfma && a->n_q >= kMfmaMinQueries) return VECTRA_VARIANT_MFMA;
   return stream_chunks(a) ? VECTRA_VARIANT_STREAM : VECTRA_VARIANT_GENERIC;
 }
 
@@ -198,6 +206,9 @@ int vectra_rbf_attention_fwd(const vectra_rbf_args* a, vectra_stream_t stream) {
   switch (variant) {
     case VECTRA_VARIANT_STREAM:
       err = vectra::launch_stream(p, a->in_dtype, a->out_dtype, stream_chunks(a), s);
+      break;
+    case VECTRA_VARIANT_MFMA:
+      err = vectra::launch_mfma(p, a->in_dtype, a->out_dtype, s);
       break;
     default:
       err = vectra::launch_generic(p, a->in_dtype, a->out_dtype, s);

@@ -16,6 +16,11 @@ hipError_t launch_stream(Problem& p, int in_dtype, int out_dtype, int chunks, hi
 // Generic kernel: any strides and sizes.
 hipError_t launch_generic(Problem& p, int in_dtype, int out_dtype, hipStream_t s);
 
+// MFMA kernel: bf16/fp16 inputs, output in the input dtype or fp32,
+// D == Dv in {16, 32, 64, 128}, unit d stride, 16-byte rows, Nk >= 1.
+bool mfma_supports(const Problem& p, int in_dtype, int out_dtype);
+hipError_t launch_mfma(Problem& p, int in_dtype, int out_dtype, hipStream_t s);
+
 hipError_t launch_squared_norms(const void* x, int dtype, int64_t B, int64_t H, int64_t N,
                                 int64_t D, const int64_t* strides, float* out, hipStream_t s);
 
