@@ -70,15 +70,41 @@ def parse_args():
     return p.parse_args()
 
 
+# The eager chain materialises [.., Nq, Nk, D] in fp32; the CPU sample is
+# bounded to this many elements of that tensor (a slice of planes and query
+# rows), and its rate converted to subjects per second.
+CPU_SAMPLE_ELEMENTS = 1 << 26
+
+
+def cpu_sample(config, inputs):
+    """(sliced inputs, batches, heads, query rows) the CPU leg runs on."""
+    per_row = config.n_k * config.head_dim
+    rows_cap = max(1, CPU_SAMPLE_ELEMENTS // per_row)
+    batches, heads, n_q = config.batch, config.heads, config.n_q
+    if batches * heads * n_q > rows_cap:
+        batches = max(1, rows_cap // (heads * n_q))
+    if batches * heads * n_q > rows_cap:
+        heads = max(1, rows_cap // n_q)
+    if batches * heads * n_q > rows_cap:
+        n_q = rows_cap
+    bias = inputs.key_bias[:batches, :heads] if inputs.key_bias is not None else None
+    scale = inputs.scale
+    if scale.dim() == 4 and scale.shape[1] > 1:
+        scale = scale[:, :heads]
+    sliced = configs.Inputs(inputs.q[:batches, :heads, :n_q], inputs.k[:batches, :heads],
+                            inputs.v[:batches, :heads], scale, bias, None)
+    return sliced, batches, heads, n_q
+
+
 def cpu_baseline(config, host_inputs, seconds):
     """Times the eager chain (the oracle's restatement of the reference's
     reference.py:54-58) in torch fp32 on the host cores; returns (record,
-    output on the sample)."""
+    sample slice, output on the sample)."""
     from oracle import rbf as oracle  # noqa: E402  (cpu_baseline leg only)
 
     threads = torch.get_num_threads()
-    sample = host_inputs
-    chunk = 64 if config.n_q > 1 else None
+    sample, batches, heads, n_q = cpu_sample(config, host_inputs)
+    chunk = 64 if n_q > 1 else None
     out = oracle.eager_fp32(*sample.args(), batch_chunk=chunk)  # warm-up + reference
     reps, start = 0, time.perf_counter()
     while True:
@@ -87,7 +113,8 @@ def cpu_baseline(config, host_inputs, seconds):
         elapsed = time.perf_counter() - start
         if elapsed >= seconds:
             break
-    qps = sample.q.shape[0] * reps / elapsed
+    rows_per_s = batches * heads * n_q * reps / elapsed
+    qps = rows_per_s / (config.heads * config.n_q)  # subjects per second
     cpu_model = 'unknown'
     try:
         with open('/proc/cpuinfo', encoding='utf-8') as f:
@@ -97,6 +124,7 @@ def cpu_baseline(config, host_inputs, seconds):
                     break
     except OSError:
         pass
+    whole = (batches, heads, n_q) == (config.batch, config.heads, config.n_q)
     record = {
         'value': qps,
         'unit': 'queries/s',
@@ -104,11 +132,13 @@ def cpu_baseline(config, host_inputs, seconds):
         'kind': 'port',
         'sample': (
             f'eager chain (sub, pow, sum, scale, bias, softmax, matmul) in torch fp32 on '
-            f'{sample.q.shape[0]} subjects of input set 0 (bf16 inputs upcast), '
+            + (f'all {config.batch} subjects' if whole else
+               f'{batches} subject(s) x {heads} head(s) x {n_q} query row(s), scaled to subjects')
+            + f' of input set 0 ({"bf16" if config.dtype == torch.bfloat16 else "input"} values upcast), '
             f'{reps} reps in {elapsed:.1f}s on {threads} threads of {cpu_model}'
         ),
     }
-    return record, out
+    return record, (batches, heads, n_q), out
 
 
 def main():
@@ -141,7 +171,7 @@ def main():
     # ---- CPU baseline leg (also the numerics reference). ----
     cpu = None
     if args.cpu_seconds > 0:
-        cpu, want = cpu_baseline(config, host0, args.cpu_seconds)
+        cpu, (nb, nh, nr), want = cpu_baseline(config, host0, args.cpu_seconds)
         log(f'cpu baseline: {cpu["value"]:.4g} queries/s on {cpu["cores"]} threads')
 
     # ---- Numerics gate (before any timing). ----
@@ -152,7 +182,8 @@ def main():
         raise SystemExit('numerics gate: operator output is not the rounded fp32 result')
     if cpu is not None:
         tol = (1e-5, 1e-6) if config.dtype == torch.float32 else (1e-3, 1e-4)
-        torch.testing.assert_close(fp32.cpu(), want, rtol=tol[0], atol=tol[1], equal_nan=True)
+        torch.testing.assert_close(fp32[:nb, :nh, :nr].cpu(), want, rtol=tol[0], atol=tol[1],
+                                   equal_nan=True)
         log('numerics gate passed against the eager chain')
 
     probe = capi.make_args(*[t for t in (sets[0].q, sets[0].k, sets[0].v)], fp32,
@@ -200,7 +231,8 @@ def main():
     ms = start.elapsed_time(end) / args.steps
     seconds = ms / 1e3
     fused = roofline.fused_bytes(shape)
-    mfma_bound = config.n_q >= 1024
+    # Bound of the workload: HBM unless its intensity is above the ridge.
+    mfma_bound = roofline.analyze(shape)['fused_is_memory_bound'] is False
     if mfma_bound:
         achieved = roofline.matrix_flops(shape) / seconds / 1e12
         line_roof = {'bound': 'mfma', 'achieved': achieved,

@@ -77,7 +77,7 @@ __global__ __launch_bounds__(512) void rbf_mfma_kernel(Problem p, int32_t q_bloc
   constexpr int kDvTiles = kDv / 16;
   constexpr int kDChunks = kD / 8;      // 16-byte chunks per K row
   constexpr int kDvChunks = kDv / 8;
-  static_assert(kD % 8 == 0 && kDv % 16 == 0 && kKeys % 32 == 0, "tile shape");
+  static_assert(kD % 8 == 0 && kDv % 16 == 0 && kKeys % 32 == 0 && kKeys <= 128, "tile shape");
 
   extern __shared__ __align__(16) unsigned char lds[];
   T* k_lds = reinterpret_cast<T*>(lds);
@@ -277,13 +277,15 @@ hipError_t launch_mfma_k(Problem& p, hipStream_t s) {
 
 template <typename T, typename OutT, int kD>
 hipError_t launch_mfma_d(Problem& p, hipStream_t s) {
-  // Key tile with the least padding of Nk (ties to the larger tile).
-  const int64_t pad32 = (p.Nk + 31) / 32 * 32, pad64 = (p.Nk + 63) / 64 * 64,
-                pad128 = (p.Nk + 127) / 128 * 128;
-  // 128-key tiles only up to 64 head dims (their LDS tile stays under 64 KB).
-  if (kD <= 64 && pad128 <= pad64 && pad128 <= pad32) return launch_mfma_k<T, OutT, kD, 128>(p, s);
-  if (pad64 <= pad32) return launch_mfma_k<T, OutT, kD, 64>(p, s);
-  return launch_mfma_k<T, OutT, kD, 32>(p, s);
+  // Key axes up to 128 run as one tile (one global round trip, two barriers)
+  // of the smallest multiple of 32 keys that covers them; longer axes stream
+  // tiles of 64 keys (128 up to 64 head dims; the LDS tile stays under 64 KB).
+  const int64_t n_k = p.Nk;
+  if (n_k <= 32) return launch_mfma_k<T, OutT, kD, 32>(p, s);
+  if (n_k <= 64) return launch_mfma_k<T, OutT, kD, 64>(p, s);
+  if (n_k <= 96) return launch_mfma_k<T, OutT, kD, 96>(p, s);
+  if (kD <= 64) return launch_mfma_k<T, OutT, kD, 128>(p, s);
+  return launch_mfma_k<T, OutT, kD, 64>(p, s);
 }
 
 template <typename T, typename OutT>
