@@ -267,6 +267,32 @@ def test_bias_and_scale_dtypes(bias_dtype, scale_dtype):
         np.testing.assert_allclose(got, want, **FP32_TOL)
 
 
+@pytest.mark.parametrize('n_q', [1, 40])
+@pytest.mark.parametrize('bias_dtype', [torch.float16, torch.bfloat16])
+def test_two_byte_bias_planes_at_any_alignment(bias_dtype, n_q):
+    # An odd key count puts every other (b, h) plane of a 2-byte bias at an
+    # address = 2 (mod 4); a view one element into a buffer does the same for
+    # the base pointer.  The kernels read biases as aligned 32-bit words.
+    gen = torch.Generator().manual_seed(13)
+    batch, heads, n_k = 3, 2, 41
+    q = torch.randn(batch, heads, n_q, 32, generator=gen).bfloat16()
+    k = torch.randn(batch, heads, n_k, 32, generator=gen).bfloat16()
+    v = torch.randn(batch, heads, n_k, 32, generator=gen).bfloat16()
+    flat = (2.0 * torch.randn(batch * heads * n_k + 1, generator=gen)).to(bias_dtype)
+    flat[::7] = -math.inf
+    flat_gpu = flat.cuda()
+    for offset in (0, 1):
+        bias_gpu = flat_gpu[offset:offset + batch * heads * n_k].view(batch, heads, 1, n_k)
+        assert (bias_gpu.data_ptr() % 4 == 0) == (offset == 0)
+        bias = flat[offset:offset + batch * heads * n_k].view(batch, heads, 1, n_k)
+        want = oracle.expanded_fp64(q, k, v, torch.tensor(0.05), bias.float())
+        for variant in _variants(q, k, v, torch.tensor(0.05), bias):
+            got = capi.forward(q.cuda(), k.cuda(), v.cuda(), torch.tensor(0.05).cuda(), bias_gpu,
+                               out_dtype=torch.float32, variant=variant)
+            np.testing.assert_allclose(got.cpu().double().numpy(), want, err_msg=f'{variant} offset {offset}',
+                                       **HALF_TOL)
+
+
 def test_empty_key_set_gives_zeros():
     q = torch.randn(1, 2, 3, 32)
     k, v = torch.empty(1, 2, 0, 32), torch.empty(1, 2, 0, 32)

@@ -98,6 +98,7 @@ struct StreamSlot {
   uint4 k[kPasses];
   uint4 v[kPasses];
   uint32_t bias[kPasses];  // aligned words holding the key biases
+  uint32_t bias_misalign;  // address & 3 of the row's bias plane (wave-uniform)
   uint4 q;
   RawScalar scale;
 };
@@ -146,7 +147,6 @@ void rbf_stream_kernel(Problem p) {
   const uint32_t v_row_bytes = static_cast<uint32_t>(p.sv[2]) * sizeof(T);
   const bool has_bias = p.bias != nullptr;
   const int32_t bias_esize = p.bias_dtype == VECTRA_F32 ? 4 : 2;
-  const uint32_t bias_misalign = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p.bias) & 3);
 
   if (n_k == 0) {  // softmax over no keys contributes nothing (eager gives 0)
     for (int32_t row = wave_id; row < total_rows; row += n_waves) {
@@ -197,9 +197,10 @@ void rbf_stream_kernel(Problem p) {
     if (has_bias) {
       const char* bp = reinterpret_cast<const char*>(p.bias) +
                        (c.b * p.sbb + c.h * p.sbh) * bias_esize;
+      slot.bias_misalign = base_misalign(bp);
 #pragma unroll
       for (int s = 0; s < kPasses; ++s)
-        slot.bias[s] = load_raw_scalar32(bp, bias_misalign, o.bias[s], p.bias_dtype).word;
+        slot.bias[s] = load_raw_scalar32(bp, slot.bias_misalign, o.bias[s], p.bias_dtype).word;
     }
     if (tile == 0) {
       const char* qp = reinterpret_cast<const char*>(p.q) +
@@ -240,7 +241,7 @@ void rbf_stream_kernel(Problem p) {
         // Position of a 2-byte bias inside its word, from the key index
         // (the same arithmetic as the load).
         const uint32_t key = static_cast<uint32_t>(j < n_k - 1 ? j : n_k - 1);
-        const uint32_t bytes = key * static_cast<uint32_t>(p.sbn) * bias_esize + bias_misalign;
+        const uint32_t bytes = key * static_cast<uint32_t>(p.sbn) * bias_esize + slot.bias_misalign;
         x += decode_raw_scalar(RawScalar{slot.bias[s], (bytes & 2u) * 8u}, p.bias_dtype);
       }
       x = live[s] ? x : -INFINITY;

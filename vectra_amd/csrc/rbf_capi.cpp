@@ -20,8 +20,26 @@
 #include "rbf_kernels.h"
 #include "vectra_rbf.h"
 
+namespace vectra {
+
+void make_fast_div(int64_t d, uint32_t* mul, uint32_t* shift) {
+  uint32_t l = 0;
+  while ((int64_t{1} << l) < d) ++l;  // l = ceil(log2 d)
+  if ((int64_t{1} << l) == d) {
+    *mul = 0;
+    *shift = l;
+    return;
+  }
+  *mul = static_cast<uint32_t>(((uint64_t{1} << (31 + l)) + static_cast<uint64_t>(d) - 1) /
+                               static_cast<uint64_t>(d));
+  *shift = l - 1;
+}
+
+}  // namespace vectra
+
 namespace {
 
+using vectra::make_fast_div;
 using vectra::Problem;
 
 constexpr int kAbiMajor = 1;
@@ -82,20 +100,6 @@ int validate(const vectra_rbf_args* a) {
   // Kernels index query rows with 32-bit wave ids.
   if (rows > 0x7fffffffLL) return VECTRA_ERR_TOO_LARGE;
   return VECTRA_OK;
-}
-
-// Multiplier and shift for vectra::fast_div (division of 31-bit values by d).
-void make_fast_div(int64_t d, uint32_t* mul, uint32_t* shift) {
-  uint32_t l = 0;
-  while ((int64_t{1} << l) < d) ++l;  // l = ceil(log2 d)
-  if ((int64_t{1} << l) == d) {
-    *mul = 0;
-    *shift = l;
-    return;
-  }
-  *mul = static_cast<uint32_t>(((uint64_t{1} << (31 + l)) + static_cast<uint64_t>(d) - 1) /
-                               static_cast<uint64_t>(d));
-  *shift = l - 1;
 }
 
 Problem make_problem(const vectra_rbf_args* a) {
@@ -200,7 +204,8 @@ int vectra_rbf_attention_fwd(const vectra_rbf_args* a, vectra_stream_t stream) {
   if (variant < 0) return -variant;
   Problem p = make_problem(a);
   // Wave budget for the persistent stream kernel (it sizes its own grid).
-  p.grid_waves = device_compute_units() * stream_waves_per_cu();
+  p.compute_units = device_compute_units();
+  p.grid_waves = p.compute_units * stream_waves_per_cu();
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t err = hipErrorInvalidValue;
   switch (variant) {

@@ -29,6 +29,7 @@ struct Problem {
   int64_t sbb, sbh, sbn;
   int64_t total_rows;  // B * H * Nq
   int32_t grid_waves;  // waves launched by persistent kernels (<= total_rows)
+  int32_t compute_units;  // of the device the launch runs on
   uint32_t nq_mul, nq_shift;  // FastDiv of Nq (see fast_div)
   uint32_t h_mul, h_shift;    // FastDiv of H
 };
@@ -98,14 +99,21 @@ __device__ __forceinline__ RawScalar load_raw_scalar(const void* base, int64_t i
   return r;
 }
 
-// Same, for an element at a 32-bit element offset from a (wave-uniform) base:
-// the address becomes base + 32-bit lane offset, which the global_load
-// instruction encodes directly.
+// Same, for an element at a 32-bit element offset from a wave-uniform base
+// that is only 2-byte aligned (a (b, h) plane of a 2-byte bias starts
+// wherever the batch and head strides put it).  The word read is the aligned
+// 32-bit word holding the element, never the bytes after it; the address is
+// aligned base + 32-bit lane offset, which global_load encodes directly.
+// `misalign` must be base_misalign(base); decodes recompute the shift from it.
+__device__ __forceinline__ uint32_t base_misalign(const char* base) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(base) & 3);
+}
+
 __device__ __forceinline__ RawScalar load_raw_scalar32(const char* base, uint32_t misalign,
                                                        uint32_t elem_offset, int32_t dtype) {
   const uint32_t bytes = elem_offset * (dtype == VECTRA_F32 ? 4u : 2u) + misalign;
   RawScalar r;
-  r.word = *reinterpret_cast<const uint32_t*>(base + (bytes & ~3u));
+  r.word = *reinterpret_cast<const uint32_t*>(base - misalign + (bytes & ~3u));
   r.shift = (bytes & 2u) * 8u;
   return r;
 }

@@ -8,6 +8,9 @@ namespace vectra {
 
 struct Problem;
 
+// Multiplier and shift for fast_div (division of 31-bit values by d >= 1).
+void make_fast_div(int64_t d, uint32_t* mul, uint32_t* shift);
+
 // Stream kernel: requires unit element stride in d for q, k, v and out,
 // 16-byte-aligned rows, D == Dv == chunks * (16 / sizeof(input element)),
 // chunks in {2, 4, 8, 16}.

@@ -1,0 +1,8 @@
+// MFMA kernels for __bf16 inputs and float outputs (see rbf_mfma_impl.h).
+#include "rbf_mfma_impl.h"
+
+namespace vectra {
+
+hipError_t launch_mfma_bf16_f32(Problem& p, hipStream_t s) { return launch_mfma_t<__bf16, float>(p, s); }
+
+}  // namespace vectra
