@@ -26,6 +26,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -58,7 +59,7 @@ def log(*args):
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.split('\n\n')[0])
     p.add_argument('--gpus', type=int, default=1)
-    p.add_argument('--steps', type=int, default=200)
+    p.add_argument('--steps', type=int, default=2000)
     p.add_argument('--warmup', type=int, default=20)
     p.add_argument('--config', default='serving', choices=sorted(configs.CONFIGS))
     p.add_argument('--dtype', default=None, choices=['bf16', 'fp16', 'fp32'])
@@ -67,6 +68,8 @@ def parse_args():
                    help='CPU-baseline budget (0 skips the CPU leg; numerics then use the '
                    'bit-exact rounding check only)')
     p.add_argument('--sets', type=int, default=0, help='input sets to rotate (0: auto)')
+    p.add_argument('--no-read-ceiling', action='store_true',
+                   help='skip the plain-read ceiling measurement')
     return p.parse_args()
 
 
@@ -125,6 +128,17 @@ def cpu_baseline(config, host_inputs, seconds):
     except OSError:
         pass
     whole = (batches, heads, n_q) == (config.batch, config.heads, config.n_q)
+    # The operator's own CPU path (the C++ kernel behind the CPU dispatch key)
+    # on the same sample, in the input dtype.
+    torch.ops.vectra.rbf_attention(*sample.args())
+    op_reps, op_start = 0, time.perf_counter()
+    while True:
+        torch.ops.vectra.rbf_attention(*sample.args())
+        op_reps += 1
+        op_elapsed = time.perf_counter() - op_start
+        if op_elapsed >= seconds / 2:
+            break
+    op_qps = batches * heads * n_q * op_reps / op_elapsed / (config.heads * config.n_q)
     record = {
         'value': qps,
         'unit': 'queries/s',
@@ -137,8 +151,70 @@ def cpu_baseline(config, host_inputs, seconds):
             + f' of input set 0 ({"bf16" if config.dtype == torch.bfloat16 else "input"} values upcast), '
             f'{reps} reps in {elapsed:.1f}s on {threads} threads of {cpu_model}'
         ),
+        'op_cpu_path': {'value': op_qps, 'unit': 'queries/s', 'reps': op_reps,
+                        'note': 'torch.ops.vectra.rbf_attention on CPU tensors (fused C++ loop), same sample'},
     }
     return record, (batches, heads, n_q), out
+
+
+# The K timed steps run as trials of this many launches (the last trial takes
+# any remainder); the reported time per step is the median over trials.
+TRIAL_STEPS = 100
+
+
+def time_trials(step, steps, warmup, stream, graph=True):
+    """Milliseconds per step of each trial of the K = `steps` timed launches.
+
+    Each trial is one HIP-graph replay of its launches (or a host loop with
+    graph=False), bracketed by events on `stream`, the stream the kernels run
+    on; the K launches are bracketed by synchronisations on both sides.
+    """
+    sizes = [TRIAL_STEPS] * (steps // TRIAL_STEPS) + ([steps % TRIAL_STEPS] if steps % TRIAL_STEPS else [])
+    if graph:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for i in range(3):
+                step(i)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graphs = {}
+        warm = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(warm):
+            for i in range(max(warmup, 1)):
+                step(i)
+        for size in set(sizes):
+            graphs[size] = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graphs[size]):
+                for i in range(size):
+                    step(i)
+        warm.replay()
+    else:
+        for i in range(warmup):
+            step(i)
+    torch.cuda.synchronize()
+    events = []
+    for size in sizes:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        if graph:
+            graphs[size].replay()
+        else:
+            for i in range(size):
+                step(i)
+        end.record(stream)
+        events.append((size, start, end))
+    torch.cuda.synchronize()
+    return [start.elapsed_time(end) / size for size, start, end in events]
+
+
+def load_profile(name):
+    """A committed JSON summary under profiles/, or None."""
+    path = os.path.join(ROOT, 'profiles', name)
+    if not os.path.exists(path):
+        return None
+    with open(path, encoding='utf-8') as f:
+        return json.load(f)
 
 
 def main():
@@ -195,40 +271,8 @@ def main():
         return torch.ops.vectra.rbf_attention(*sets[i % n_sets].args())
 
     stream = torch.cuda.current_stream()
-    if args.no_graph:
-        for i in range(args.warmup):
-            step(i)
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for i in range(args.steps):
-            step(i)
-        end.record(stream)
-        torch.cuda.synchronize()
-    else:
-        side = torch.cuda.Stream()
-        side.wait_stream(stream)
-        with torch.cuda.stream(side):
-            for i in range(3):
-                step(i)
-        stream.wait_stream(side)
-        torch.cuda.synchronize()
-        warm, timed = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-        with torch.cuda.graph(warm):
-            for i in range(max(args.warmup, 1)):
-                step(i)
-        with torch.cuda.graph(timed):
-            for i in range(args.steps):
-                step(i)
-        warm.replay()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        timed.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-
-    ms = start.elapsed_time(end) / args.steps
+    trial_ms = time_trials(step, args.steps, args.warmup, stream, graph=not args.no_graph)
+    ms = statistics.median(trial_ms)
     seconds = ms / 1e3
     fused = roofline.fused_bytes(shape)
     # Bound of the workload: HBM unless its intensity is above the ridge.
@@ -247,13 +291,26 @@ def main():
     # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     # runs of this workload (profiles/traffic_<config>.json, made by
     # vectra_amd.benchmarks.rocprof_summary), if they measured this kernel.
-    traffic_path = os.path.join(ROOT, 'profiles', f'traffic_{config.name}.json')
-    if os.path.exists(traffic_path):
-        with open(traffic_path, encoding='utf-8') as f:
-            measured = json.load(f)
-        if measured.get('kernel') == line_roof['kernel']:
-            line_roof['traffic'] = measured['traffic_bytes']
-            line_roof['traffic_source'] = os.path.relpath(traffic_path, ROOT)
+    measured = load_profile(f'traffic_{config.name}.json')
+    if measured is not None and measured.get('kernel') == line_roof['kernel']:
+        line_roof['traffic'] = measured['traffic_bytes']
+        line_roof['traffic_source'] = f'profiles/traffic_{config.name}.json'
+    # Measured bytes of the operator over those of the eager chain at the same
+    # shape (profiles/bytes_ratio_<config>.json, rocprof_summary ratio).
+    ratio = load_profile(f'bytes_ratio_{config.name}.json')
+    if ratio is not None:
+        line_roof['bytes_ratio_vs_eager'] = ratio['bytes_ratio']
+        line_roof['bytes_ratio_source'] = f'profiles/bytes_ratio_{config.name}.json'
+    # A plain streaming read of the same number of bytes, timed the same way:
+    # the practical ceiling for an HBM-bound kernel.
+    if not mfma_bound and not args.no_read_ceiling:
+        from vectra_amd.benchmarks import read_ceiling  # noqa: E402
+
+        ceiling = read_ceiling.measure(fused)
+        line_roof['read_ceiling'] = {'us': ceiling['us'], 'GB/s': ceiling['GB/s'],
+                                     'frac_of_peak': ceiling['GB/s'] / line_roof['peak'],
+                                     'kernel_over_ceiling': achieved / ceiling['GB/s']}
+        log(f'read ceiling: {ceiling["us"]:.2f} us, {ceiling["GB/s"]:.0f} GB/s')
     line_roof['algorithmic_bytes'] = fused
 
     result = {
@@ -274,7 +331,9 @@ def main():
                         f'Lk={config.n_k} D={config.head_dim}',
             'batch': config.batch, 'heads': config.heads, 'n_q': config.n_q, 'n_k': config.n_k,
             'head_dim': config.head_dim, 'input_sets': n_sets,
-            'timing': 'host loop' if args.no_graph else 'hip graph of K launches',
+            'timing': ('median over trials of %d launches, each %s' %
+                       (min(TRIAL_STEPS, args.steps), 'a host loop' if args.no_graph else 'one HIP-graph replay')),
+            'trials': len(trial_ms),
             'variant': variant,
         },
         'roofline': line_roof,

@@ -1,0 +1,86 @@
+"""The eager operator chain on the GPU, beside the fused operator.
+
+  python -m vectra_amd.benchmarks.eager_gpu --impl eager|fused [--config serving] [--reps 20]
+
+`eager_rbf_attention` restates the reference's eager chain
+(kernels/vectra_kernels/reference.py:46-58): the [B, H, Lq, Lk, D]
+difference, its square and sum, `-d * scale (+ bias)`, softmax and the
+product with v, each a separate kernel.  For 16-bit inputs the coefficient
+is cast to the input dtype first, as the reference's benchmarks do
+(kernels/benchmarks/throughput.py:129-131), so the chain stays in that dtype.
+
+The script runs the chosen implementation `--reps` times over rotating input
+sets (after one warm-up call per set) and prints one JSON line with the
+median time per call and the number of calls made.  Under
+`rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` the counters summed
+over every dispatch of the run, divided by that number of calls, are the
+measured HBM bytes of one call of the region; `rocprof_summary region`
+does the arithmetic.  Inputs are built on the host and copied, so the run's
+only kernels are the region's own (and the runtime's copy blits, which the
+summary excludes).
+"""
+
+import argparse
+import json
+import statistics
+
+import torch
+
+from vectra_amd.benchmarks import configs
+import vectra_amd.kernels  # noqa: F401  (registers torch.ops.vectra.rbf_attention)
+
+
+def eager_rbf_attention(q, k, v, scale, key_bias=None):
+    """The unfused chain, in the inputs' dtype (reference.py:54-58)."""
+    if q.dtype != torch.float32:
+        scale = scale.to(q.dtype)
+    sq_dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-1)
+    logits = -sq_dist * scale
+    if key_bias is not None:
+        logits = logits + key_bias
+    return torch.softmax(logits, dim=-1) @ v
+
+
+def fused(q, k, v, scale, key_bias=None):
+    return torch.ops.vectra.rbf_attention(q, k, v, scale, key_bias)
+
+
+IMPLS = {'eager': eager_rbf_attention, 'fused': fused}
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument('--impl', choices=sorted(IMPLS), required=True)
+    p.add_argument('--config', default='serving', choices=sorted(configs.CONFIGS))
+    p.add_argument('--sets', type=int, default=5)
+    p.add_argument('--reps', type=int, default=20)
+    args = p.parse_args()
+    config = configs.CONFIGS[args.config]
+    fn = IMPLS[args.impl]
+    sets = [configs.make_inputs(config, seed=s).to('cuda') for s in range(args.sets)]
+    calls = 0
+    for s in sets:
+        fn(*s.args())
+        calls += 1
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    times = []
+    for i in range(args.reps):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        fn(*sets[i % args.sets].args())
+        end.record(stream)
+        end.synchronize()
+        calls += 1
+        times.append(start.elapsed_time(end))
+    print(json.dumps({
+        'impl': args.impl,
+        'config': config.name,
+        'calls': calls,
+        'median_ms': statistics.median(times),
+        'dtype': str(config.dtype).replace('torch.', ''),
+    }), flush=True)
+
+
+if __name__ == '__main__':
+    main()
