@@ -83,6 +83,12 @@ def test_struct_layout_is_accepted():
         ({'d': 32, 'dv': 16}, 'generic'),  # D != Dv
         ({'d': 7, 'dv': 7}, 'generic'),
         ({'base': (1 << 20) + 2}, 'generic'),  # misaligned rows
+        ({'n_q': 65, 'n_k': 65}, 'mfma'),  # self-attention over a comparable set
+        ({'n_q': 65, 'n_k': 65, 'dtype': torch.float32}, 'mfma'),  # the same in fp32
+        ({'n_q': 65, 'n_k': 65, 'dtype': torch.float16, 'out_dtype': torch.float32}, 'mfma'),
+        ({'n_q': 4096, 'n_k': 4096, 'd': 64, 'dv': 64}, 'mfma'),  # long key axis
+        ({'n_q': 65, 'n_k': 65, 'd': 48, 'dv': 48}, 'generic'),  # no MFMA tile for 48 dims
+        ({'n_q': 15, 'n_k': 65}, 'stream'),  # under one query tile: rows stream two key tiles
     ],
 )
 def test_variant_selection(kwargs, variant):

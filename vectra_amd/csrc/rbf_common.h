@@ -290,7 +290,7 @@ struct OpMax {
 };
 
 // All-reduce over the low lane bits 1 .. kGroup/2 (groups of kGroup adjacent
-// lanes; kGroup a power of two <= 16).  Mirrors are valid because the lower
+// lanes; kGroup a power of two <= 64).  Mirrors are valid because the lower
 // bits are already reduced when they run.
 template <int kGroup, typename Op>
 __device__ __forceinline__ float reduce_low(float x, Op op) {
@@ -298,6 +298,8 @@ __device__ __forceinline__ float reduce_low(float x, Op op) {
   if constexpr (kGroup >= 4) x = op(x, dpp<0x4E>(x));
   if constexpr (kGroup >= 8) x = op(x, dpp<0x141>(x));
   if constexpr (kGroup >= 16) x = op(x, dpp<0x140>(x));
+  if constexpr (kGroup >= 32) x = allreduce_bit16(x, op);
+  if constexpr (kGroup >= 64) x = allreduce_bit32(x, op);
   return x;
 }
 

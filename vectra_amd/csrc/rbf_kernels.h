@@ -19,7 +19,7 @@ hipError_t launch_stream(Problem& p, int in_dtype, int out_dtype, int chunks, hi
 // Generic kernel: any strides and sizes.
 hipError_t launch_generic(Problem& p, int in_dtype, int out_dtype, hipStream_t s);
 
-// MFMA kernel: bf16/fp16 inputs, output in the input dtype or fp32,
+// MFMA kernel: bf16/fp16/fp32 inputs, output in the input dtype or fp32,
 // D == Dv in {16, 32, 64, 128}, unit d stride, 16-byte rows, Nk >= 1.
 bool mfma_supports(const Problem& p, int in_dtype, int out_dtype);
 hipError_t launch_mfma(Problem& p, int in_dtype, int out_dtype, hipStream_t s);

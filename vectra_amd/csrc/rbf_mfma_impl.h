@@ -1,30 +1,36 @@
-// Query-tile RBF attention on gfx950 matrix cores (bf16 / fp16 inputs):
-// the kernel template.  Instantiated per dtype pair in rbf_mfma_<in>_<out>.hip.
+// Query-tile RBF attention on gfx950 matrix cores: the kernel template.
+// Instantiated per dtype pair in rbf_mfma_<in>_<out>.hip.
 //
 // For query tiles (Nq >= 16: self-attention over a comparable set, long key
-// axes) both products run on v_mfma_f32_16x16x32_{bf16,f16}:
+// axes) both products run on MFMA, transposed so that no operand has to move
+// between lanes:
 //
-//   S^T = K . Q^T     (16 keys x 16 queries per MFMA, 32 head dims deep)
-//   O^T = V^T . P^T   (16 value dims x 16 queries, 32 keys deep)
+//   S^T = K . Q^T     (16 keys x 16 queries per instruction)
+//   O^T = V^T . P^T   (16 value dims x 16 queries)
 //
-// Lane layouts (checked on the device): for A (16 x 32) lane l holds row
-// l % 16, elements 8 (l / 16) .. +7 of the deep dimension; for B (32 x 16)
-// column l % 16, the same 8 deep elements; the fp32 result C (16 x 16) gives
-// lane l column l % 16, rows 4 (l / 16) + r, r = 0..3.
+// Lane layouts of the instructions used (wave64, l = lane, g = l / 16):
+//   16x16x32 bf16/f16  A: row l % 16, deep 8g .. 8g+7;  B: column l % 16, same
+//   16x16x16 bf16/f16  A: row l % 16, deep 4g .. 4g+3;  B: column l % 16, same
+//   16x16x4  f32       A: row l % 16, deep g;           B: column l % 16, deep g
+//   result C (16 x 16 fp32): column l % 16, rows 4g .. 4g+3.
 //
-// Computing S transposed puts, in each lane, the scores of ONE query (column
-// l % 16) against keys 4 (l / 16) + r of each 16-key block.  Those eight
-// values for two adjacent blocks are exactly the B operand of the second
-// product once the 32-key deep dimension is read in the permuted order
-// {4g..4g+3, 16+4g..16+4g+3} for lane group g = l / 16 -- and V^T is read in
-// the same order from LDS.  So P never moves between lanes, and the online
-// softmax state (running max, sum, rescale) of a query lives in its four
-// lanes l, l+16, l+32, l+48, reduced with gfx950 permlane swaps.
+// S^T puts in each lane the scores of ONE query (column l % 16) against keys
+// 16t + 4g + r (r = 0..3) of every 16-key block t.  Those four weights are
+// exactly the B operand of a 16x16x16 step over block t (deep index 4g + r),
+// and, one r at a time, of a 16x16x4 f32 step (deep index g).  So P stays in
+// the registers it was computed in, and the softmax state of a query lives
+// in its four lanes l, l+16, l+32, l+48, reduced with gfx950 permlane swaps.
 //
-// P is fed to the second product as a bf16 (or fp16) hi + lo pair (two
-// MFMAs), so the weights keep ~16 more bits than one rounding would: rounding
-// P once (as the reference's Triton kernel does) misses the rtol 1e-3 gate at
-// a few tens of keys.
+// The distance is folded into the first product: its accumulator starts at
+// -(|q|^2 + |k|^2) / 2, so the result is S' = q.k - (|q|^2 + |k|^2) / 2 =
+// -d / 2, and the logit (in log2 units) is
+//   2 gamma log2(e) min(S', 0) + bias log2(e)  =  log2(e) (-gamma max(d, 0) + bias).
+//
+// 16-bit inputs: P is fed to the second product as a hi + lo pair of 16-bit
+// values (two MFMAs), so the weights keep ~16 more bits than one rounding
+// would; rounding P once (as the reference's Triton kernel does) misses the
+// rtol 1e-3 gate at a few tens of keys.  fp32 inputs: both products run on
+// the fp32 MFMA, exact products with fp32 accumulation.
 //
 // Semantics are those of rbf_stream_kernel: clamp of the distance at 0,
 // -scale * d + bias, keys >= Nk masked, a running max replaced by 0 while it
@@ -41,79 +47,134 @@ namespace vectra {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// The two products for one input type.  `Qk` is a 16-byte fragment of a K
+// or Q row; `Pv` a 4-element operand of the second product.
 template <typename T>
-struct Mfma;
+struct MfmaOps;
 
 template <>
-struct Mfma<__bf16> {
-  typedef __bf16 vec8 __attribute__((ext_vector_type(8)));
-  static __device__ __forceinline__ f32x4 run(vec8 a, vec8 b, f32x4 c) {
+struct MfmaOps<__bf16> {
+  typedef __bf16 Qk __attribute__((ext_vector_type(8)));
+  typedef short Pv __attribute__((ext_vector_type(4)));  // four bf16 bit patterns
+  static __device__ __forceinline__ f32x4 qk(Qk a, Qk b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
+  static __device__ __forceinline__ f32x4 pv(Pv a, Pv b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ short bits(__bf16 x) { return __builtin_bit_cast(short, x); }
 };
 
 template <>
-struct Mfma<_Float16> {
-  typedef _Float16 vec8 __attribute__((ext_vector_type(8)));
-  static __device__ __forceinline__ f32x4 run(vec8 a, vec8 b, f32x4 c) {
+struct MfmaOps<_Float16> {
+  typedef _Float16 Qk __attribute__((ext_vector_type(8)));
+  typedef _Float16 Pv __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f32x4 qk(Qk a, Qk b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 pv(Pv a, Pv b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ _Float16 bits(_Float16 x) { return x; }
+};
+
+template <>
+struct MfmaOps<float> {
+  static __device__ __forceinline__ f32x4 mma(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
 };
 
-// LDS tile geometry.  Row pads make the 16 rows one operand read touches
-// start in distinct banks.
-template <typename T, int kD, int kDv, int kKeys>
+// Splits four fp32 weights into 16-bit hi and lo parts (hi + lo = w to ~2^-17).
+template <typename T>
+__device__ __forceinline__ void split_weights(const float* w, typename MfmaOps<T>::Pv& hi,
+                                              typename MfmaOps<T>::Pv& lo) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const T h = static_cast<T>(w[r]);
+    hi[r] = MfmaOps<T>::bits(h);
+    lo[r] = MfmaOps<T>::bits(static_cast<T>(w[r] - static_cast<float>(h)));
+  }
+}
+
+// LDS tile geometry.
+//   K: row-major [key][head dim], 16-bit rows padded to whole 32-deep steps
+//      (zeros) plus 8, fp32 rows plus 4: the 16 rows one operand read touches
+//      start in distinct banks.
+//   V: 16-bit transposed [value dim][key] (row stride kKeys + 4), read as
+//      4 consecutive keys; fp32 as [key / 4][value dim][key % 4], read as the
+//      4 keys 16t + 4g + 0..3 of one value dim.
+//   Then -|k|^2 / 2 and the bias (log2 units, -inf past Nk) per key.
+template <typename T, int kD, int kKeys>
 struct MfmaTile {
-  static constexpr int kKSteps = (kD + 31) / 32;   // deep steps of S^T = K . Q^T
-  static constexpr int kDpad = kKSteps * 32;       // head dim padded with zeros
-  static constexpr int kKStride = kDpad + 8;       // K row stride (elements)
-  static constexpr int kVStride = kKeys + 4;       // V^T row stride (elements)
-  static constexpr int kKBytes = kKeys * kKStride * sizeof(T);
-  static constexpr int kVBytes = kDv * kVStride * sizeof(T);
-  static constexpr int kBytes = kKBytes + kVBytes + 2 * kKeys * sizeof(float);
+  static constexpr bool kHalf = sizeof(T) == 2;
+  static constexpr int kKSteps = kHalf ? (kD + 31) / 32 : kD / 4;  // deep steps of S^T
+  static constexpr int kDpad = kHalf ? (kD + 31) / 32 * 32 : kD;
+  static constexpr int kKStride = kDpad + (kHalf ? 8 : 4);
+  static constexpr int kVStride = kKeys + 4;  // 16-bit V^T rows
+  static constexpr int kKBytes = kKeys * kKStride * static_cast<int>(sizeof(T));
+  static constexpr int kVBytes = kHalf ? kD * kVStride * 2 : kKeys * kD * 4;
+  static constexpr int kBytes = kKBytes + kVBytes + 2 * kKeys * static_cast<int>(sizeof(float));
 };
 
 // Work item: one (b, h) plane and one block of kWaves * 16 query rows; the
 // plane's keys are streamed in tiles of kKeys.  The grid is persistent: a
 // workgroup takes items blockIdx.x, blockIdx.x + gridDim.x, ...  Every
-// thread owns fixed load slots of a tile (K rows, V row pairs, biases, and
-// at an item's first tile its q fragment).  All of them are issued together
-// into registers as soon as the previous tile has been copied to LDS, so the
-// next tile's HBM latency overlaps this tile's products and softmax.
-template <typename T, int kD, int kDv, int kKeys, int kWaves>
+// thread owns fixed load slots of a tile (16-byte chunks of K rows, of V rows
+// -- pairs of rows for 16-bit inputs, which are transposed two keys per
+// 32-bit LDS write -- and biases, plus at an item's first tile its q
+// fragment).  All of them are issued together into registers as soon as the
+// previous tile is in LDS, so the next tile's HBM latency overlaps this
+// tile's products and softmax.
+template <typename T, int kD, int kKeys, int kWaves>
 struct MfmaStage {
+  static constexpr bool kHalf = sizeof(T) == 2;
   static constexpr int kThreads = 64 * kWaves;
-  static constexpr int kDChunks = kD / 8;
-  static constexpr int kDvChunks = kDv / 8;
-  static constexpr int kKSteps = (kD + 31) / 32;
+  static constexpr int kVec = 16 / static_cast<int>(sizeof(T));
+  static constexpr int kDChunks = kD / kVec;  // 16-byte chunks per row
+  static constexpr int kVRows = kHalf ? 2 : 1;
   static constexpr int kKSlots = (kKeys * kDChunks + kThreads - 1) / kThreads;
-  static constexpr int kVSlots = ((kKeys / 2) * kDvChunks + kThreads - 1) / kThreads;
+  static constexpr int kVSlots = ((kKeys / kVRows) * kDChunks + kThreads - 1) / kThreads;
   static constexpr int kBSlots = (kKeys + kThreads - 1) / kThreads;
+  // q chunks per lane: 16-bit, one per 32-deep step; fp32, the D / 4
+  // consecutive dims of lane group g.
+  static constexpr int kQChunks = kHalf ? (kD + 31) / 32 : kD / 16;
   uint4 k[kKSlots];
-  uint4 v[kVSlots][2];  // rows 2p and 2p + 1 of one 16-byte column chunk
+  uint4 v[kVSlots][kVRows];
   uint32_t bias[kBSlots];
   uint32_t bias_misalign;  // address & 3 of the item's bias plane
-  uint4 q[kKSteps];
+  uint4 q[kQChunks];
   RawScalar scale;
 };
 
-template <typename T, typename OutT, int kD, int kDv, int kKeys, int kWaves>
+// Byte offsets, inside a (b, h) plane, of a thread's load slots for one tile.
+template <typename T, int kD, int kKeys, int kWaves>
+struct MfmaOffsets {
+  using Stage = MfmaStage<T, kD, kKeys, kWaves>;
+  uint32_t k[Stage::kKSlots];
+  uint32_t v[Stage::kVSlots][Stage::kVRows];
+  uint32_t bias[Stage::kBSlots];  // elements
+};
+
+template <typename T, typename OutT, int kD, int kKeys, int kWaves>
 __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_t q_blocks) {
-  using Geo = MfmaTile<T, kD, kDv, kKeys>;
-  using Stage = MfmaStage<T, kD, kDv, kKeys, kWaves>;
-  using Vec8 = typename Mfma<T>::vec8;
+  using Geo = MfmaTile<T, kD, kKeys>;
+  using Stage = MfmaStage<T, kD, kKeys, kWaves>;
+  using Offsets = MfmaOffsets<T, kD, kKeys, kWaves>;
+  constexpr bool kHalf = Geo::kHalf;
   constexpr int kThreads = Stage::kThreads;
-  constexpr int kNTiles = kKeys / 16;   // 16-key blocks per tile
-  constexpr int kPSteps = kKeys / 32;   // deep steps of O^T = V^T . P^T
-  constexpr int kDvTiles = kDv / 16;
+  constexpr int kVec = Stage::kVec;
   constexpr int kDChunks = Stage::kDChunks;
-  constexpr int kDvChunks = Stage::kDvChunks;
-  static_assert(kD % 8 == 0 && kDv % 16 == 0 && kKeys % 32 == 0 && kKeys <= 128, "tile shape");
+  constexpr int kVRows = Stage::kVRows;
+  constexpr int kNTiles = kKeys / 16;  // 16-key blocks per tile
+  constexpr int kDvTiles = kD / 16;
+  constexpr int kESize = static_cast<int>(sizeof(T));
+  static_assert(kD % 16 == 0 && kKeys % 16 == 0 && kKeys <= 128, "tile shape");
   static_assert(64 % kDChunks == 0, "a K row's chunks stay inside one wave");
 
   extern __shared__ __align__(16) unsigned char lds[];
   T* k_lds = reinterpret_cast<T*>(lds);
-  T* vt_lds = reinterpret_cast<T*>(lds + Geo::kKBytes);
+  T* v_lds = reinterpret_cast<T*>(lds + Geo::kKBytes);
   float* kn_lds = reinterpret_cast<float*>(lds + Geo::kKBytes + Geo::kVBytes);
   float* bias_lds = kn_lds + kKeys;
 
@@ -129,6 +190,12 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
   const int32_t tiles = (n_k + kKeys - 1) / kKeys;
   const bool has_bias = p.bias != nullptr;
   const int32_t bias_esize = p.bias_dtype == VECTRA_F32 ? 4 : 2;
+  const uint32_t k_row_bytes = static_cast<uint32_t>(p.sk[2]) * kESize;
+  const uint32_t v_row_bytes = static_cast<uint32_t>(p.sv[2]) * kESize;
+  const uint32_t q_row_bytes = static_cast<uint32_t>(p.sq[2]) * kESize;
+  // Contiguous output rows take one vector store per 4 values.
+  const bool out_vec = p.so[3] == 1 && p.so[2] % 4 == 0 && p.so[1] % 4 == 0 && p.so[0] % 4 == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.out) & 15u) == 0;
 
   struct Coords {
     int32_t b, h, qb;
@@ -142,7 +209,35 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
     return c;
   };
 
-  // Padding columns of the K tile (head dims kD .. kDpad) stay zero.
+  // Rows past Nk read row Nk - 1 (in bounds) and are masked in LDS.
+  auto tile_offsets = [&](int32_t tile) {
+    Offsets o;
+    const int32_t j0 = tile * kKeys;
+#pragma unroll
+    for (int s = 0; s < Stage::kKSlots; ++s) {
+      const int slot = tid + s * kThreads;
+      const uint32_t j = static_cast<uint32_t>(min(j0 + slot / kDChunks, n_k - 1));
+      o.k[s] = j * k_row_bytes + (slot % kDChunks) * 16u;
+    }
+#pragma unroll
+    for (int s = 0; s < Stage::kVSlots; ++s) {
+      const int slot = tid + s * kThreads;
+#pragma unroll
+      for (int e = 0; e < kVRows; ++e) {
+        const uint32_t j = static_cast<uint32_t>(min(j0 + kVRows * (slot / kDChunks) + e, n_k - 1));
+        o.v[s][e] = j * v_row_bytes + (slot % kDChunks) * 16u;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < Stage::kBSlots; ++s) {
+      const uint32_t j = static_cast<uint32_t>(min(j0 + tid + s * kThreads, n_k - 1));
+      o.bias[s] = j * static_cast<uint32_t>(p.sbn);
+    }
+    return o;
+  };
+  const Offsets first = tile_offsets(0);
+
+  // Padding columns of 16-bit K rows (head dims kD .. kDpad) stay zero.
   if constexpr (Geo::kDpad > kD) {
     for (int i = tid; i < kKeys * (Geo::kDpad - kD); i += kThreads) {
       const int key = i / (Geo::kDpad - kD);
@@ -150,57 +245,44 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
     }
   }
 
-  // Issues every load of (item, tile) into `st`.  Rows past Nk read row
-  // Nk - 1 (in bounds) and are masked when written to LDS.
+  // Issues every load of (item, tile) into `st`.
   auto issue = [&](Stage& st, int32_t item, int32_t tile) {
     const Coords c = coords(item);
-    const T* k_plane = static_cast<const T*>(p.k) + c.b * p.sk[0] + c.h * p.sk[1];
-    const T* v_plane = static_cast<const T*>(p.v) + c.b * p.sv[0] + c.h * p.sv[1];
-    const int32_t j0 = tile * kKeys;
+    const char* kp = static_cast<const char*>(p.k) + (c.b * p.sk[0] + c.h * p.sk[1]) * kESize;
+    const char* vp = static_cast<const char*>(p.v) + (c.b * p.sv[0] + c.h * p.sv[1]) * kESize;
+    const Offsets o = tile == 0 ? first : tile_offsets(tile);
 #pragma unroll
-    for (int s = 0; s < Stage::kKSlots; ++s) {
-      const int slot = tid + s * kThreads;
-      const int key = slot / kDChunks;
-      const int32_t j = min(j0 + key, n_k - 1);
-      if (slot < kKeys * kDChunks) st.k[s] = load16_stream(k_plane + j * p.sk[2] + (slot % kDChunks) * 8);
-    }
+    for (int s = 0; s < Stage::kKSlots; ++s)
+      if (tid + s * kThreads < kKeys * kDChunks) st.k[s] = load16_stream(kp + o.k[s]);
 #pragma unroll
     for (int s = 0; s < Stage::kVSlots; ++s) {
-      const int slot = tid + s * kThreads;
-      const int pair = slot / kDvChunks;
-      const int32_t j = j0 + 2 * pair;
-      if (slot < (kKeys / 2) * kDvChunks) {
-        const T* src = v_plane + (slot % kDvChunks) * 8;
-        st.v[s][0] = load16_stream(src + min(j, n_k - 1) * p.sv[2]);
-        st.v[s][1] = load16_stream(src + min(j + 1, n_k - 1) * p.sv[2]);
+      if (tid + s * kThreads < (kKeys / kVRows) * kDChunks) {
+#pragma unroll
+        for (int e = 0; e < kVRows; ++e) st.v[s][e] = load16_stream(vp + o.v[s][e]);
       }
     }
     if (has_bias) {
-      const char* bp = reinterpret_cast<const char*>(p.bias) + (c.b * p.sbb + c.h * p.sbh) * bias_esize;
+      const char* bp = static_cast<const char*>(p.bias) + (c.b * p.sbb + c.h * p.sbh) * bias_esize;
       st.bias_misalign = base_misalign(bp);
 #pragma unroll
-      for (int s = 0; s < Stage::kBSlots; ++s) {
-        const int key = tid + s * kThreads;
-        const uint32_t j = static_cast<uint32_t>(min(j0 + key, n_k - 1));
-        if (key < kKeys)
-          st.bias[s] = load_raw_scalar32(bp, st.bias_misalign, j * static_cast<uint32_t>(p.sbn), p.bias_dtype).word;
-      }
+      for (int s = 0; s < Stage::kBSlots; ++s)
+        if (tid + s * kThreads < kKeys)
+          st.bias[s] = load_raw_scalar32(bp, st.bias_misalign, o.bias[s], p.bias_dtype).word;
     }
     if (tile == 0) {
-      const int32_t q_row = (c.qb * kWaves + wave) * 16 + col;
-      const T* q_src = static_cast<const T*>(p.q) + c.b * p.sq[0] + c.h * p.sq[1] +
-                       min(q_row, n_q - 1) * p.sq[2];
+      const int32_t q_row = min((c.qb * kWaves + wave) * 16 + col, n_q - 1);
+      const char* qp = static_cast<const char*>(p.q) + (c.b * p.sq[0] + c.h * p.sq[1]) * kESize;
+      const uint32_t q_off = static_cast<uint32_t>(q_row) * q_row_bytes;
 #pragma unroll
-      for (int ks = 0; ks < Geo::kKSteps; ++ks) {
-        const int d0 = 32 * ks + 8 * grp;
-        if (d0 < kD) st.q[ks] = load16(q_src + d0);
+      for (int i = 0; i < Stage::kQChunks; ++i) {
+        const int d0 = kHalf ? 32 * i + 8 * grp : grp * (kD / 4) + 4 * i;
+        if (d0 < kD) st.q[i] = load16(qp + q_off + d0 * kESize);
       }
       st.scale = load_raw_scalar(p.scale, c.b * p.ssb + c.h * p.ssh, p.scale_dtype);
     }
   };
 
-  // Copies a staged tile into LDS: K rows and their norms, V transposed (two
-  // keys per 32-bit write), biases as fp32 with keys past Nk at -inf.
+  // Copies a staged tile into LDS: K rows and -|k|^2 / 2, V, and biases.
   auto publish = [&](const Stage& st, int32_t tile) {
     const int32_t j0 = tile * kKeys;
 #pragma unroll
@@ -209,28 +291,37 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
       if (Stage::kKSlots * kThreads == kKeys * kDChunks || slot < kKeys * kDChunks) {
         const int key = slot / kDChunks;
         const uint4 raw = j0 + key < n_k ? st.k[s] : make_uint4(0, 0, 0, 0);
-        *reinterpret_cast<uint4*>(k_lds + key * Geo::kKStride + (slot % kDChunks) * 8) = raw;
+        *reinterpret_cast<uint4*>(k_lds + key * Geo::kKStride + (slot % kDChunks) * kVec) = raw;
         const float sq = reduce_low<kDChunks>(dot_chunk<T>(raw, raw, 0.f), OpSum());
-        if (slot % kDChunks == 0) kn_lds[key] = sq;
+        if (slot % kDChunks == 0) kn_lds[key] = -0.5f * sq;
       }
     }
 #pragma unroll
     for (int s = 0; s < Stage::kVSlots; ++s) {
       const int slot = tid + s * kThreads;
-      if (slot < (kKeys / 2) * kDvChunks) {
-        const int pair = slot / kDvChunks;
-        const int d0 = (slot % kDvChunks) * 8;
-        const uint4 r0 = j0 + 2 * pair < n_k ? st.v[s][0] : make_uint4(0, 0, 0, 0);
-        const uint4 r1 = j0 + 2 * pair + 1 < n_k ? st.v[s][1] : make_uint4(0, 0, 0, 0);
-        const uint32_t w0[4] = {r0.x, r0.y, r0.z, r0.w};
-        const uint32_t w1[4] = {r1.x, r1.y, r1.z, r1.w};
+      if (slot < (kKeys / kVRows) * kDChunks) {
+        const int row = kVRows * (slot / kDChunks);  // first key of the slot
+        const int d0 = (slot % kDChunks) * kVec;
+        if constexpr (kHalf) {
+          const uint4 r0 = j0 + row < n_k ? st.v[s][0] : make_uint4(0, 0, 0, 0);
+          const uint4 r1 = j0 + row + 1 < n_k ? st.v[s][1] : make_uint4(0, 0, 0, 0);
+          const uint32_t w0[4] = {r0.x, r0.y, r0.z, r0.w};
+          const uint32_t w1[4] = {r1.x, r1.y, r1.z, r1.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // Elements 2e and 2e+1 of the chunk, for keys 2p (low half) and 2p+1.
-          const uint32_t even = (w0[e] & 0xffffu) | (w1[e] << 16);
-          const uint32_t odd = (w0[e] >> 16) | (w1[e] & 0xffff0000u);
-          *reinterpret_cast<uint32_t*>(vt_lds + (d0 + 2 * e) * Geo::kVStride + 2 * pair) = even;
-          *reinterpret_cast<uint32_t*>(vt_lds + (d0 + 2 * e + 1) * Geo::kVStride + 2 * pair) = odd;
+          for (int e = 0; e < 4; ++e) {
+            // Elements 2e and 2e+1 of the chunk for keys row (low half) and row + 1.
+            const uint32_t even = (w0[e] & 0xffffu) | (w1[e] << 16);
+            const uint32_t odd = (w0[e] >> 16) | (w1[e] & 0xffff0000u);
+            *reinterpret_cast<uint32_t*>(v_lds + (d0 + 2 * e) * Geo::kVStride + row) = even;
+            *reinterpret_cast<uint32_t*>(v_lds + (d0 + 2 * e + 1) * Geo::kVStride + row) = odd;
+          }
+        } else {
+          const uint4 r0 = j0 + row < n_k ? st.v[s][0] : make_uint4(0, 0, 0, 0);
+          float* dst = reinterpret_cast<float*>(v_lds) + ((row >> 2) * kD + d0) * 4 + (row & 3);
+          dst[0] = __uint_as_float(r0.x);
+          dst[4] = __uint_as_float(r0.y);
+          dst[8] = __uint_as_float(r0.z);
+          dst[12] = __uint_as_float(r0.w);
         }
       }
     }
@@ -244,7 +335,7 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
           if (has_bias) {
             const uint32_t j = static_cast<uint32_t>(j0 + key);
             const uint32_t bytes = j * static_cast<uint32_t>(p.sbn) * bias_esize + st.bias_misalign;
-            x = decode_raw_scalar(RawScalar{st.bias[s], (bytes & 2u) * 8u}, p.bias_dtype);
+            x = decode_raw_scalar(RawScalar{st.bias[s], (bytes & 2u) * 8u}, p.bias_dtype) * kLog2e;
           }
         }
         bias_lds[key] = x;
@@ -252,8 +343,8 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
     }
   };
 
-  Vec8 q_frag[Geo::kKSteps];
-  float q_norm = 0.f, neg_scale = 0.f, run_max = -INFINITY, run_sum = 0.f;
+  uint4 q_frag[Stage::kQChunks];
+  float q_half = 0.f, coef = 0.f, run_max = -INFINITY, run_sum = 0.f;
   f32x4 acc[kDvTiles];
 
   Stage st;
@@ -271,16 +362,15 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
     if (tile == 0) {
       const Coords c = coords(item);
       const bool q_live = (c.qb * kWaves + wave) * 16 + col < n_q;
-      q_norm = 0.f;
+      float q_norm = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < Geo::kKSteps; ++ks) {
-        const bool in_d = 32 * ks + 8 * grp < kD;
-        const uint4 raw = (q_live && in_d) ? st.q[ks] : make_uint4(0, 0, 0, 0);
-        q_frag[ks] = __builtin_bit_cast(Vec8, raw);
-        q_norm = dot_chunk<T>(raw, raw, q_norm);
+      for (int i = 0; i < Stage::kQChunks; ++i) {
+        const int d0 = kHalf ? 32 * i + 8 * grp : grp * (kD / 4) + 4 * i;
+        q_frag[i] = (q_live && d0 < kD) ? st.q[i] : make_uint4(0, 0, 0, 0);
+        q_norm = dot_chunk<T>(q_frag[i], q_frag[i], q_norm);
       }
-      q_norm = allreduce_bit32(allreduce_bit16(q_norm, OpSum()), OpSum());
-      neg_scale = -decode_raw_scalar(st.scale, p.scale_dtype);
+      q_half = -0.5f * allreduce_bit32(allreduce_bit16(q_norm, OpSum()), OpSum());
+      coef = 2.f * kLog2e * decode_raw_scalar(st.scale, p.scale_dtype);
       run_max = -INFINITY;
       run_sum = 0.f;
 #pragma unroll
@@ -290,25 +380,36 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
     const bool more = next_item < items;
     if (more) issue(st, next_item, next_tile);  // in flight while this tile is reduced
 
-    // Scores S^T for this lane's query against keys 16t + 4g + r.
+    // Logits (log2 units) of this lane's query against keys 16t + 4g + r.
     float logit[kNTiles][4];
     float tile_max = -INFINITY;
 #pragma unroll
     for (int t = 0; t < kNTiles; ++t) {
-      f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < Geo::kKSteps; ++ks) {
-        const Vec8 a = *reinterpret_cast<const Vec8*>(k_lds + (16 * t + col) * Geo::kKStride + 32 * ks + 8 * grp);
-        sc = Mfma<T>::run(a, q_frag[ks], sc);
-      }
       const float4 kn = *reinterpret_cast<const float4*>(kn_lds + 16 * t + 4 * grp);
+      f32x4 sc = f32x4{kn.x + q_half, kn.y + q_half, kn.z + q_half, kn.w + q_half};
+      if constexpr (kHalf) {
+        using Qk = typename MfmaOps<T>::Qk;
+#pragma unroll
+        for (int ks = 0; ks < Geo::kKSteps; ++ks) {
+          const Qk a = *reinterpret_cast<const Qk*>(k_lds + (16 * t + col) * Geo::kKStride + 32 * ks + 8 * grp);
+          sc = MfmaOps<T>::qk(a, __builtin_bit_cast(Qk, q_frag[ks]), sc);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kD / 16; ++i) {
+          const float4 kf = *reinterpret_cast<const float4*>(
+              reinterpret_cast<const float*>(k_lds) + (16 * t + col) * Geo::kKStride + grp * (kD / 4) + 4 * i);
+          sc = MfmaOps<float>::mma(kf.x, __uint_as_float(q_frag[i].x), sc);
+          sc = MfmaOps<float>::mma(kf.y, __uint_as_float(q_frag[i].y), sc);
+          sc = MfmaOps<float>::mma(kf.z, __uint_as_float(q_frag[i].z), sc);
+          sc = MfmaOps<float>::mma(kf.w, __uint_as_float(q_frag[i].w), sc);
+        }
+      }
       const float4 bias = *reinterpret_cast<const float4*>(bias_lds + 16 * t + 4 * grp);
-      const float knv[4] = {kn.x, kn.y, kn.z, kn.w};
       const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float dist = fmaxf((q_norm + knv[r]) - 2.f * sc[r], 0.f);
-        const float x = neg_scale * dist + bv[r];
+        const float x = fmaf(coef, fminf(sc[r], 0.f), bv[r]);
         logit[t][r] = x;
         tile_max = fmaxf(tile_max, x);
       }
@@ -316,35 +417,41 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
     tile_max = allreduce_bit32(allreduce_bit16(tile_max, OpMax()), OpMax());
     const float new_max = fmaxf(run_max, tile_max);
     const float safe_max = new_max == -INFINITY ? 0.f : new_max;
-    const float alpha = __builtin_amdgcn_exp2f((run_max - safe_max) * kLog2e);
+    const float alpha = __builtin_amdgcn_exp2f(run_max - safe_max);
     run_max = new_max;
     run_sum *= alpha;
 #pragma unroll
     for (int u = 0; u < kDvTiles; ++u) acc[u] *= alpha;
 
-    // O^T += V^T . P^T, 32 keys per step, P as a hi + lo pair.
+    // O^T += V^T . P^T, one 16-key block at a time.
 #pragma unroll
-    for (int ps = 0; ps < kPSteps; ++ps) {
-      Vec8 p_hi, p_lo;
+    for (int t = 0; t < kNTiles; ++t) {
+      float w[4];
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float w = __builtin_amdgcn_exp2f((logit[2 * ps + half][r] - safe_max) * kLog2e);
-          run_sum += w;
-          const T hi = static_cast<T>(w);
-          p_hi[4 * half + r] = hi;
-          p_lo[4 * half + r] = static_cast<T>(w - static_cast<float>(hi));
-        }
+      for (int r = 0; r < 4; ++r) {
+        w[r] = __builtin_amdgcn_exp2f(logit[t][r] - safe_max);
+        run_sum += w[r];
       }
+      if constexpr (kHalf) {
+        using Pv = typename MfmaOps<T>::Pv;
+        Pv p_hi, p_lo;
+        split_weights<T>(w, p_hi, p_lo);
 #pragma unroll
-      for (int u = 0; u < kDvTiles; ++u) {
-        const T* row = vt_lds + (16 * u + col) * Geo::kVStride + 32 * ps + 4 * grp;
-        const uint2 lo4 = *reinterpret_cast<const uint2*>(row);
-        const uint2 hi4 = *reinterpret_cast<const uint2*>(row + 16);
-        const Vec8 a = __builtin_bit_cast(Vec8, make_uint4(lo4.x, lo4.y, hi4.x, hi4.y));
-        acc[u] = Mfma<T>::run(a, p_hi, acc[u]);
-        acc[u] = Mfma<T>::run(a, p_lo, acc[u]);
+        for (int u = 0; u < kDvTiles; ++u) {
+          const Pv a = *reinterpret_cast<const Pv*>(v_lds + (16 * u + col) * Geo::kVStride + 16 * t + 4 * grp);
+          acc[u] = MfmaOps<T>::pv(a, p_hi, acc[u]);
+          acc[u] = MfmaOps<T>::pv(a, p_lo, acc[u]);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < kDvTiles; ++u) {
+          const float4 vv = *reinterpret_cast<const float4*>(
+              reinterpret_cast<const float*>(v_lds) + ((4 * t + grp) * kD + 16 * u + col) * 4);
+          acc[u] = MfmaOps<float>::mma(vv.x, w[0], acc[u]);
+          acc[u] = MfmaOps<float>::mma(vv.y, w[1], acc[u]);
+          acc[u] = MfmaOps<float>::mma(vv.z, w[2], acc[u]);
+          acc[u] = MfmaOps<float>::mma(vv.w, w[3], acc[u]);
+        }
       }
     }
 
@@ -358,8 +465,20 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
         OutT* o = static_cast<OutT*>(p.out) + c.b * p.so[0] + c.h * p.so[1] + q_row * p.so[2];
 #pragma unroll
         for (int u = 0; u < kDvTiles; ++u) {
+          OutT vals[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[(16 * u + 4 * grp + r) * p.so[3]] = from_float<OutT>(acc[u][r] * inv);
+          for (int r = 0; r < 4; ++r) vals[r] = from_float<OutT>(acc[u][r] * inv);
+          OutT* dst = o + (16 * u + 4 * grp) * p.so[3];
+          if (out_vec) {
+            if constexpr (sizeof(OutT) == 4) {
+              *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(vals);
+            } else {
+              *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(vals);
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[r * p.so[3]] = vals[r];
+          }
         }
       }
     }
@@ -368,7 +487,6 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
     tile = next_tile;
   }
 }
-
 
 // ------------------------------------------------------------------- host
 
@@ -379,9 +497,9 @@ int mfma_resident_blocks() {
   static std::atomic<int> cached{0};
   int n = cached.load(std::memory_order_relaxed);
   if (n == 0) {
-    using Geo = MfmaTile<T, kD, kD, kKeys>;
+    using Geo = MfmaTile<T, kD, kKeys>;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &n, reinterpret_cast<const void*>(&rbf_mfma_kernel<T, OutT, kD, kD, kKeys, kWaves>), 64 * kWaves,
+            &n, reinterpret_cast<const void*>(&rbf_mfma_kernel<T, OutT, kD, kKeys, kWaves>), 64 * kWaves,
             Geo::kBytes) != hipSuccess ||
         n < 1)
       n = 1;
@@ -395,7 +513,7 @@ int mfma_resident_blocks() {
 // products.
 template <typename T, typename OutT, int kD, int kKeys, int kWaves>
 hipError_t launch_mfma_w(Problem& p, hipStream_t s) {
-  using Geo = MfmaTile<T, kD, kD, kKeys>;
+  using Geo = MfmaTile<T, kD, kKeys>;
   const int32_t q_blocks = static_cast<int32_t>((p.Nq + kWaves * 16 - 1) / (kWaves * 16));
   const int64_t items = p.B * p.H * q_blocks;
   int64_t blocks = static_cast<int64_t>(mfma_resident_blocks<T, OutT, kD, kKeys, kWaves>()) *
@@ -407,7 +525,7 @@ hipError_t launch_mfma_w(Problem& p, hipStream_t s) {
   make_fast_div(q_blocks, &k.nq_mul, &k.nq_shift);
   int32_t qb = q_blocks;
   void* args[] = {&k, &qb};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&rbf_mfma_kernel<T, OutT, kD, kD, kKeys, kWaves>),
+  return hipLaunchKernel(reinterpret_cast<const void*>(&rbf_mfma_kernel<T, OutT, kD, kKeys, kWaves>),
                          dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves), args, Geo::kBytes, s);
 }
 
@@ -422,17 +540,32 @@ hipError_t launch_mfma_k(Problem& p, hipStream_t s) {
   return launch_mfma_w<T, OutT, kD, kKeys, 8>(p, s);
 }
 
+// Longest key tile per input type and head dim (register staging and LDS,
+// chosen so that no instantiation spills): 128 keys, 64 for 16-bit 128-dim
+// heads and fp32 64-dim heads, 32 for fp32 128-dim heads.
+template <typename T, int kD>
+constexpr int mfma_max_keys() {
+  if constexpr (sizeof(T) == 2) return kD <= 64 ? 128 : 64;
+  return kD <= 32 ? 128 : (kD == 64 ? 64 : 32);
+}
+
 template <typename T, typename OutT, int kD>
 hipError_t launch_mfma_d(Problem& p, hipStream_t s) {
-  // Key axes up to 128 run as one tile (one global round trip per item) of
-  // 64, 96 or 128 keys, the smallest that covers them; longer axes stream
-  // 128-key tiles.  128 head dims use 64-key tiles (register staging).
-  if constexpr (kD >= 128) {
-    return launch_mfma_k<T, OutT, kD, 64>(p, s);
+  // Key axes that fit one tile run as one tile (one global round trip per
+  // item) of 32, 64, 80 or 128 keys, the smallest that covers them; longer
+  // axes stream tiles of the longest size.
+  constexpr int kMax = mfma_max_keys<T, kD>();
+  if constexpr (kMax == 32) {
+    return launch_mfma_k<T, OutT, kD, 32>(p, s);
   } else {
-    if (p.Nk <= 64) return launch_mfma_k<T, OutT, kD, 64>(p, s);
-    if (p.Nk <= 96) return launch_mfma_k<T, OutT, kD, 96>(p, s);
-    return launch_mfma_k<T, OutT, kD, 128>(p, s);
+    if (p.Nk <= 32) return launch_mfma_k<T, OutT, kD, 32>(p, s);
+    if constexpr (kMax >= 128) {
+      if (p.Nk <= 64) return launch_mfma_k<T, OutT, kD, 64>(p, s);
+      if (p.Nk <= 80) return launch_mfma_k<T, OutT, kD, 80>(p, s);
+      return launch_mfma_k<T, OutT, kD, 128>(p, s);
+    } else {
+      return launch_mfma_k<T, OutT, kD, 64>(p, s);
+    }
   }
 }
 
@@ -452,5 +585,6 @@ hipError_t launch_mfma_bf16_bf16(Problem& p, hipStream_t s);
 hipError_t launch_mfma_bf16_f32(Problem& p, hipStream_t s);
 hipError_t launch_mfma_f16_f16(Problem& p, hipStream_t s);
 hipError_t launch_mfma_f16_f32(Problem& p, hipStream_t s);
+hipError_t launch_mfma_f32_f32(Problem& p, hipStream_t s);
 
 }  // namespace vectra
