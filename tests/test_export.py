@@ -1,0 +1,125 @@
+"""Deployment compile: checkpoints, bundle export and load, padded serving (CPU).
+
+Restates the reference's models/tests/test_train_and_export.py:66-120
+(checkpoint round trip, export-verify-serve, tampered bundle) on CPU
+Inductor, plus the toolchain check and the numerics gate itself.
+"""
+
+import json
+import os
+import shutil
+
+import pytest
+import torch
+
+from vectra_amd.export import compile_entry
+from vectra_amd.price_transformer import checkpoint
+from vectra_amd.price_transformer import model as model_lib
+
+CONFIG = model_lib.ModelConfig(d_model=64, num_heads=2, num_layers=2, ffn_dim=128, num_candidates=24)
+SPEC = compile_entry.ServingSpec('cpu', batch_size=8, block_dtype='float32')
+
+
+@pytest.fixture(autouse=True)
+def _fresh_dynamo():
+    torch._dynamo.reset()  # pylint: disable=protected-access
+    yield
+    torch._dynamo.reset()  # pylint: disable=protected-access
+
+
+@pytest.fixture(scope='module', name='trained')
+def _trained(tmp_path_factory):
+    torch.manual_seed(0)
+    model = model_lib.PriceTransformer(CONFIG).eval()
+    directory = str(tmp_path_factory.mktemp('ckpt'))
+    checkpoint.save(directory, model, metadata={'note': 'random init'})
+    return model, directory
+
+
+@pytest.fixture(scope='module', name='bundle')
+def _bundle(trained, tmp_path_factory):
+    _, directory = trained
+    out = str(tmp_path_factory.mktemp('bundle'))
+    torch._dynamo.reset()  # pylint: disable=protected-access
+    manifest = compile_entry.export_bundle(directory, out, SPEC, numerics_batches=1)
+    return out, manifest
+
+
+def test_checkpoint_round_trip(trained):
+    model, directory = trained
+    loaded = checkpoint.load(directory)
+    assert loaded.config == model.config
+    inputs = model_lib.example_inputs(CONFIG, 6, seed=3)
+    with torch.no_grad():
+        assert torch.equal(loaded(*inputs), model(*inputs))
+    with open(os.path.join(directory, checkpoint.CONFIG), encoding='utf-8') as f:
+        assert json.load(f)['metadata'] == {'note': 'random init'}
+
+
+def test_export_bundle_compiles_verifies_and_serves(trained, bundle):
+    model, _ = trained
+    out, manifest = bundle
+    assert manifest['compile']['sites'] == CONFIG.num_layers
+    assert manifest['compile']['graph_break_count'] == 0
+    assert manifest['compile']['matches'] == {'rbf_divisor_bias_softmax[fp32]': CONFIG.num_layers}
+    assert manifest['numerics']['max_abs_error_vs_eager'] < 1e-3
+    assert set(manifest['files']) == {checkpoint.WEIGHTS, checkpoint.CONFIG}
+
+    serving = compile_entry.load_bundle(out)
+    for count in (1, 8, 13):
+        inputs = model_lib.example_inputs(CONFIG, count, seed=40 + count)
+        with torch.no_grad():
+            want = model(*inputs)
+        got = serving.predict(inputs)
+        assert got.shape == (count,)
+        torch.testing.assert_close(got, want, rtol=1e-3, atol=1e-3)
+
+
+def test_tampered_bundle_is_rejected(bundle, tmp_path):
+    out = str(tmp_path / 'tampered')
+    shutil.copytree(bundle[0], out)
+    with open(os.path.join(out, checkpoint.WEIGHTS), 'r+b') as f:
+        f.seek(-4, os.SEEK_END)
+        f.write(b'\x00\x00\x80\x7f')
+    with pytest.raises(ValueError, match='checksum'):
+        compile_entry.load_bundle(out)
+
+
+def test_toolchain_mismatch_is_rejected_unless_relaxed(bundle, tmp_path):
+    out = str(tmp_path / 'other_toolchain')
+    shutil.copytree(bundle[0], out)
+    path = os.path.join(out, compile_entry.MANIFEST)
+    with open(path, encoding='utf-8') as f:
+        manifest = json.load(f)
+    manifest['versions']['torch'] = '0.0.0'
+    with open(path, 'w', encoding='utf-8') as f:
+        json.dump(manifest, f)
+    with pytest.raises(ValueError, match='toolchain'):
+        compile_entry.load_bundle(out)
+    serving = compile_entry.load_bundle(out, strict_versions=False)
+    assert serving.spec == SPEC
+
+
+def test_unknown_bundle_format_is_rejected(bundle, tmp_path):
+    out = str(tmp_path / 'future')
+    shutil.copytree(bundle[0], out)
+    path = os.path.join(out, compile_entry.MANIFEST)
+    with open(path, encoding='utf-8') as f:
+        manifest = json.load(f)
+    manifest['format_version'] = compile_entry.FORMAT_VERSION + 1
+    with open(path, 'w', encoding='utf-8') as f:
+        json.dump(manifest, f)
+    with pytest.raises(ValueError, match='format'):
+        compile_entry.load_bundle(out)
+
+
+def test_numerics_gate_rejects_a_drifting_model(trained):
+    model, _ = trained
+
+    def drifted(*inputs):
+        return model(*inputs) + 0.05
+
+    with pytest.raises(compile_entry.NumericsError, match='differs from eager'):
+        compile_entry.max_abs_error(drifted, model, CONFIG, SPEC, batches=1)
+    worst, drift = compile_entry.max_abs_error(model, model, CONFIG, SPEC, batches=2, reference=model)
+    assert worst == 0.0 and drift == 0.0

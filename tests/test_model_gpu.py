@@ -82,3 +82,34 @@ def test_bf16_blocks_are_rewritten_and_match():
         eager_bf16 = model(*inputs)
     torch.testing.assert_close(got, eager_bf16, rtol=0, atol=3e-2)
     torch.testing.assert_close(got, fp32, rtol=0, atol=5e-2)
+
+
+@pytest.mark.timeout(900)
+def test_deployment_bundle_on_the_gpu(tmp_path):
+    # Export, reload and serve with the reference's GPU default (float16
+    # blocks): the numerics gate (rtol 1e-3 vs the eager model in the same
+    # precision) runs on the HIP operator at export and again at load.
+    from vectra_amd.export import compile_entry
+    from vectra_amd.price_transformer import checkpoint
+
+    config = _config(3)
+    torch.manual_seed(0)
+    model = model_lib.PriceTransformer(config).eval()
+    checkpoint.save(str(tmp_path / 'ckpt'), model)
+    spec = compile_entry.ServingSpec('cuda', batch_size=64, block_dtype='float16')
+    manifest = compile_entry.export_bundle(str(tmp_path / 'ckpt'), str(tmp_path / 'bundle'), spec,
+                                           numerics_batches=2)
+    print(f"manifest compile={manifest['compile']} numerics={manifest['numerics']}", flush=True)
+    assert manifest['compile']['sites'] == 3 and manifest['compile']['graph_break_count'] == 0
+    assert manifest['numerics']['max_abs_error_vs_eager'] < 1.4e-2
+    torch._dynamo.reset()  # pylint: disable=protected-access
+    serving = compile_entry.load_bundle(str(tmp_path / 'bundle'))
+    assert _native.HIP_LIBRARY in _native.loaded_libraries()
+    eager = compile_entry.prepare(checkpoint.load(str(tmp_path / 'ckpt')), spec)
+    for count in (1, 64, 100):
+        inputs = model_lib.example_inputs(config, count, seed=70 + count)
+        got = serving.predict(inputs)
+        with torch.no_grad():
+            want = eager(*inputs.to('cuda')).float()
+        assert got.shape == (count,)
+        torch.testing.assert_close(got, want, rtol=1e-3, atol=1e-3)
