@@ -15,11 +15,14 @@
 //   result C (16 x 16 fp32): column l % 16, rows 4g .. 4g+3.
 //
 // S^T puts in each lane the scores of ONE query (column l % 16) against keys
-// 16t + 4g + r (r = 0..3) of every 16-key block t.  Those four weights are
-// exactly the B operand of a 16x16x16 step over block t (deep index 4g + r),
-// and, one r at a time, of a 16x16x4 f32 step (deep index g).  So P stays in
-// the registers it was computed in, and the softmax state of a query lives
-// in its four lanes l, l+16, l+32, l+48, reduced with gfx950 permlane swaps.
+// 16t + 4g + r (r = 0..3) of every 16-key block t.  Those of blocks 2p and
+// 2p + 1 together are exactly the B operand of a 16x16x32 step over keys
+// 32p .. 32p + 31 read in the order {4g .. 4g+3, 16+4g .. 16+4g+3} (V^T is
+// read in the same order); an odd last block takes a 16x16x16 step (deep
+// index 4g + r), and fp32 takes 16x16x4 steps, one r at a time (deep index
+// g).  So P stays in the registers it was computed in, and the softmax state
+// of a query lives in its four lanes l, l+16, l+32, l+48, reduced with gfx950
+// permlane swaps.
 //
 // The distance is folded into the first product: its accumulator starts at
 // -(|q|^2 + |k|^2) / 2, so the result is S' = q.k - (|q|^2 + |k|^2) / 2 =
@@ -52,6 +55,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <typename T>
 struct MfmaOps;
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
 template <>
 struct MfmaOps<__bf16> {
   typedef __bf16 Qk __attribute__((ext_vector_type(8)));
@@ -62,7 +67,14 @@ struct MfmaOps<__bf16> {
   static __device__ __forceinline__ f32x4 pv(Pv a, Pv b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ short bits(__bf16 x) { return __builtin_bit_cast(short, x); }
+  // Two weights as packed bf16 hi (round to nearest, v_cvt_pk_bf16_f32) and
+  // lo = bf16(w - hi): hi + lo = w to ~2^-17.
+  static __device__ __forceinline__ void split2(float w0, float w1, uint32_t& hi, uint32_t& lo) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{w0, w1}, b2));
+    const float h0 = __uint_as_float(hi << 16), h1 = __uint_as_float(hi & 0xffff0000u);
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{w0 - h0, w1 - h1}, b2));
+  }
 };
 
 template <>
@@ -75,7 +87,15 @@ struct MfmaOps<_Float16> {
   static __device__ __forceinline__ f32x4 pv(Pv a, Pv b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ _Float16 bits(_Float16 x) { return x; }
+  // Two weights as packed fp16 hi (round toward zero, v_cvt_pkrtz_f16_f32)
+  // and lo = fp16(w - hi), w - hi being exact in fp32: hi + lo = w to ~2^-20.
+  static __device__ __forceinline__ void split2(float w0, float w1, uint32_t& hi, uint32_t& lo) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 h = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(w0, w1));
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(w0 - static_cast<float>(h[0]),
+                                                                 w1 - static_cast<float>(h[1])));
+  }
 };
 
 template <>
@@ -84,18 +104,6 @@ struct MfmaOps<float> {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
   }
 };
-
-// Splits four fp32 weights into 16-bit hi and lo parts (hi + lo = w to ~2^-17).
-template <typename T>
-__device__ __forceinline__ void split_weights(const float* w, typename MfmaOps<T>::Pv& hi,
-                                              typename MfmaOps<T>::Pv& lo) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const T h = static_cast<T>(w[r]);
-    hi[r] = MfmaOps<T>::bits(h);
-    lo[r] = MfmaOps<T>::bits(static_cast<T>(w[r] - static_cast<float>(h)));
-  }
-}
 
 // LDS tile geometry.
 //   K: row-major [key][head dim], 16-bit rows padded to whole 32-deep steps
@@ -408,41 +416,71 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
       const float4 bias = *reinterpret_cast<const float4*>(bias_lds + 16 * t + 4 * grp);
       const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float x = fmaf(coef, fminf(sc[r], 0.f), bv[r]);
-        logit[t][r] = x;
-        tile_max = fmaxf(tile_max, x);
-      }
+      for (int r = 0; r < 4; ++r) logit[t][r] = fmaf(coef, fminf(sc[r], 0.f), bv[r]);
+      tile_max = fmaxf(tile_max, fmaxf(fmaxf(logit[t][0], logit[t][1]), fmaxf(logit[t][2], logit[t][3])));
     }
     tile_max = allreduce_bit32(allreduce_bit16(tile_max, OpMax()), OpMax());
     const float new_max = fmaxf(run_max, tile_max);
     const float safe_max = new_max == -INFINITY ? 0.f : new_max;
     const float alpha = __builtin_amdgcn_exp2f(run_max - safe_max);
     run_max = new_max;
-    run_sum *= alpha;
+    // Rescale only when some query's maximum moved (alpha == 1 is exact).
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+      run_sum *= alpha;
 #pragma unroll
-    for (int u = 0; u < kDvTiles; ++u) acc[u] *= alpha;
+      for (int u = 0; u < kDvTiles; ++u) acc[u] *= alpha;
+    }
 
-    // O^T += V^T . P^T, one 16-key block at a time.
+    // O^T += V^T . P^T.
+    if constexpr (kHalf) {
+      using Qk = typename MfmaOps<T>::Qk;
+      using Pv = typename MfmaOps<T>::Pv;
+      // Weights of block t as packed 16-bit hi / lo pairs (keys 4g + 0,1 and 4g + 2,3).
+      auto weights = [&](int t, uint32_t* hi, uint32_t* lo) {
+        float w[4];
 #pragma unroll
-    for (int t = 0; t < kNTiles; ++t) {
-      float w[4];
+        for (int r = 0; r < 4; ++r) w[r] = __builtin_amdgcn_exp2f(logit[t][r] - safe_max);
+        run_sum += (w[0] + w[1]) + (w[2] + w[3]);
+        MfmaOps<T>::split2(w[0], w[1], hi[0], lo[0]);
+        MfmaOps<T>::split2(w[2], w[3], hi[1], lo[1]);
+      };
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        w[r] = __builtin_amdgcn_exp2f(logit[t][r] - safe_max);
-        run_sum += w[r];
+      for (int pp = 0; pp < kNTiles / 2; ++pp) {
+        uint32_t hi[4], lo[4];
+        weights(2 * pp, hi, lo);
+        weights(2 * pp + 1, hi + 2, lo + 2);
+        const Qk p_hi = __builtin_bit_cast(Qk, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+        const Qk p_lo = __builtin_bit_cast(Qk, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+#pragma unroll
+        for (int u = 0; u < kDvTiles; ++u) {
+          const T* row = v_lds + (16 * u + col) * Geo::kVStride + 32 * pp + 4 * grp;
+          const uint2 a0 = *reinterpret_cast<const uint2*>(row);
+          const uint2 a1 = *reinterpret_cast<const uint2*>(row + 16);
+          const Qk a = __builtin_bit_cast(Qk, make_uint4(a0.x, a0.y, a1.x, a1.y));
+          acc[u] = MfmaOps<T>::qk(a, p_hi, acc[u]);
+          acc[u] = MfmaOps<T>::qk(a, p_lo, acc[u]);
+        }
       }
-      if constexpr (kHalf) {
-        using Pv = typename MfmaOps<T>::Pv;
-        Pv p_hi, p_lo;
-        split_weights<T>(w, p_hi, p_lo);
+      if constexpr (kNTiles % 2 == 1) {
+        constexpr int t = kNTiles - 1;
+        uint32_t hi[2], lo[2];
+        weights(t, hi, lo);
+        const Pv p_hi = __builtin_bit_cast(Pv, make_uint2(hi[0], hi[1]));
+        const Pv p_lo = __builtin_bit_cast(Pv, make_uint2(lo[0], lo[1]));
 #pragma unroll
         for (int u = 0; u < kDvTiles; ++u) {
           const Pv a = *reinterpret_cast<const Pv*>(v_lds + (16 * u + col) * Geo::kVStride + 16 * t + 4 * grp);
           acc[u] = MfmaOps<T>::pv(a, p_hi, acc[u]);
           acc[u] = MfmaOps<T>::pv(a, p_lo, acc[u]);
         }
-      } else {
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < kNTiles; ++t) {
+        float w[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w[r] = __builtin_amdgcn_exp2f(logit[t][r] - safe_max);
+        run_sum += (w[0] + w[1]) + (w[2] + w[3]);
 #pragma unroll
         for (int u = 0; u < kDvTiles; ++u) {
           const float4 vv = *reinterpret_cast<const float4*>(
