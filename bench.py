@@ -49,6 +49,7 @@ KERNEL_NAMES = {
     'stream': 'rbf_stream_kernel',
     'generic': 'rbf_generic_kernel',
     'mfma': 'rbf_mfma_kernel',
+    'plane': 'rbf_plane_kernel',
 }
 
 

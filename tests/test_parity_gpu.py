@@ -38,7 +38,7 @@ def _variants(q, k, v, scale, bias):
     scale4, bias4 = capi.broadcast_operands(q, k, scale, bias)
     out = torch.empty((*q.shape[:-1], v.shape[-1]), device='cuda')
     found = ['auto']
-    for name in ('generic', 'stream', 'mfma'):
+    for name in ('generic', 'stream', 'mfma', 'plane'):
         if capi.select_variant(capi.make_args(q, k, v, out, scale4, bias4, name)) > 0:
             found.append(name)
     return found
@@ -125,6 +125,20 @@ def test_operator_output_is_the_rounded_fp32_result():
     assert torch.equal(out, fp32.to(torch.bfloat16))
     loaded = _native.loaded_libraries()
     assert _native.HIP_LIBRARY in loaded and _native.TORCH_LIBRARY in loaded
+
+
+@pytest.mark.parametrize('config', [configs.SERVING, configs.SELF_ATTENTION], ids=lambda c: c.name)
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16], ids=str)
+def test_every_variant_rounds_its_fp32_result_once(config, dtype):
+    """A 16-bit output is the kernel's fp32 result rounded once (no fused
+    multiply-convert), for every variant that runs the shape."""
+    inputs = configs.make_inputs(config.with_dtype(dtype), seed=3, batch=64).to('cuda')
+    for variant in _variants(*inputs.args()):
+        print(f'config={config.name} dtype={dtype} variant={variant}', flush=True)
+        fp32 = capi.forward(*inputs.args(), out_dtype=torch.float32, variant=variant)
+        half = capi.forward(*inputs.args(), out_dtype=dtype, variant=variant)
+        torch.cuda.synchronize()
+        assert torch.equal(half, fp32.to(dtype)), variant
 
 
 def test_full_serving_size_properties():

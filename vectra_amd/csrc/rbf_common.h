@@ -74,8 +74,15 @@ template <>
 __device__ __forceinline__ float to_float<__bf16>(__bf16 x) { return static_cast<float>(x); }
 
 // fp32 -> T with round-to-nearest-even (the conversion torch's .to() uses).
+// The fp32 value is made opaque first: otherwise the compiler fuses the
+// product that produced it with the conversion (v_fma_mixlo_f16, one
+// rounding), and a 16-bit output would no longer be exactly the fp32 result
+// rounded once more, as the operator's output is defined.
 template <typename T>
-__device__ __forceinline__ T from_float(float x) { return static_cast<T>(x); }
+__device__ __forceinline__ T from_float(float x) {
+  if constexpr (sizeof(T) < sizeof(float)) asm volatile("" : "+v"(x));
+  return static_cast<T>(x);
+}
 
 // A 2- or 4-byte float element fetched as the aligned 32-bit word that holds
 // it.  The load has no dtype-dependent control flow, so it can be issued

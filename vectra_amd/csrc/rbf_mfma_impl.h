@@ -8,11 +8,8 @@
 //   S^T = K . Q^T     (16 keys x 16 queries per instruction)
 //   O^T = V^T . P^T   (16 value dims x 16 queries)
 //
-// Lane layouts of the instructions used (wave64, l = lane, g = l / 16):
-//   16x16x32 bf16/f16  A: row l % 16, deep 8g .. 8g+7;  B: column l % 16, same
-//   16x16x16 bf16/f16  A: row l % 16, deep 4g .. 4g+3;  B: column l % 16, same
-//   16x16x4  f32       A: row l % 16, deep g;           B: column l % 16, deep g
-//   result C (16 x 16 fp32): column l % 16, rows 4g .. 4g+3.
+// Lane layouts of the instructions used are listed in rbf_mfma_ops.h
+// (wave64, l = lane, g = l / 16).
 //
 // S^T puts in each lane the scores of ONE query (column l % 16) against keys
 // 16t + 4g + r (r = 0..3) of every 16-key block t.  Those of blocks 2p and
@@ -45,65 +42,9 @@
 
 #include "rbf_common.h"
 #include "rbf_kernels.h"
+#include "rbf_mfma_ops.h"
 
 namespace vectra {
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-// The two products for one input type.  `Qk` is a 16-byte fragment of a K
-// or Q row; `Pv` a 4-element operand of the second product.
-template <typename T>
-struct MfmaOps;
-
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-template <>
-struct MfmaOps<__bf16> {
-  typedef __bf16 Qk __attribute__((ext_vector_type(8)));
-  typedef short Pv __attribute__((ext_vector_type(4)));  // four bf16 bit patterns
-  static __device__ __forceinline__ f32x4 qk(Qk a, Qk b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ f32x4 pv(Pv a, Pv b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-  }
-  // Two weights as packed bf16 hi (round to nearest, v_cvt_pk_bf16_f32) and
-  // lo = bf16(w - hi): hi + lo = w to ~2^-17.
-  static __device__ __forceinline__ void split2(float w0, float w1, uint32_t& hi, uint32_t& lo) {
-    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{w0, w1}, b2));
-    const float h0 = __uint_as_float(hi << 16), h1 = __uint_as_float(hi & 0xffff0000u);
-    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{w0 - h0, w1 - h1}, b2));
-  }
-};
-
-template <>
-struct MfmaOps<_Float16> {
-  typedef _Float16 Qk __attribute__((ext_vector_type(8)));
-  typedef _Float16 Pv __attribute__((ext_vector_type(4)));
-  static __device__ __forceinline__ f32x4 qk(Qk a, Qk b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ f32x4 pv(Pv a, Pv b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-  }
-  // Two weights as packed fp16 hi (round toward zero, v_cvt_pkrtz_f16_f32)
-  // and lo = fp16(w - hi), w - hi being exact in fp32: hi + lo = w to ~2^-20.
-  static __device__ __forceinline__ void split2(float w0, float w1, uint32_t& hi, uint32_t& lo) {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 h = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(w0, w1));
-    hi = __builtin_bit_cast(uint32_t, h);
-    lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(w0 - static_cast<float>(h[0]),
-                                                                 w1 - static_cast<float>(h[1])));
-  }
-};
-
-template <>
-struct MfmaOps<float> {
-  static __device__ __forceinline__ f32x4 mma(float a, float b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-  }
-};
 
 // LDS tile geometry.
 //   K: row-major [key][head dim], 16-bit rows padded to whole 32-deep steps

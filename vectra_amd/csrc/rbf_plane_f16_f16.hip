@@ -1,0 +1,8 @@
+// Plane kernels for _Float16 inputs and _Float16 outputs (see rbf_plane_impl.h).
+#include "rbf_plane_impl.h"
+
+namespace vectra {
+
+hipError_t launch_plane_f16_f16(Problem& p, hipStream_t s) { return launch_plane_t<_Float16, _Float16>(p, s); }
+
+}  // namespace vectra
