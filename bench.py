@@ -50,6 +50,7 @@ KERNEL_NAMES = {
     'generic': 'rbf_generic_kernel',
     'mfma': 'rbf_mfma_kernel',
     'plane': 'rbf_plane_kernel',
+    'tile': 'rbf_tile_kernel',
 }
 
 

@@ -62,7 +62,8 @@ enum {
   VECTRA_VARIANT_GENERIC = 1,  /* any strides / dims / dtypes               */
   VECTRA_VARIANT_STREAM = 2,   /* few query rows: HBM-scheduled, 128-bit loads */
   VECTRA_VARIANT_MFMA = 3,     /* query tiles of 16+ rows on MFMA (bf16/fp16/fp32) */
-  VECTRA_VARIANT_PLANE = 4     /* whole (b, h) planes of <= 80 rows per wave on MFMA (bf16/fp16) */
+  VECTRA_VARIANT_PLANE = 4,    /* whole (b, h) planes of <= 80 rows per wave on MFMA (bf16/fp16) */
+  VECTRA_VARIANT_TILE = 5      /* key tiles streamed through LDS, 32 query rows per wave (bf16/fp16) */
 };
 
 /*

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert capi.abi_version() == (1, 1)
+    assert capi.abi_version() == (1, 2)
     for status in range(8):
         assert capi.status_string(status)
     assert capi.status_string(capi.OK) == 'ok'
@@ -87,10 +87,12 @@ def test_struct_layout_is_accepted():
         ({'n_q': 65, 'n_k': 65, 'dtype': torch.float32}, 'mfma'),  # the same in fp32
         ({'n_q': 65, 'n_k': 65, 'dtype': torch.float16, 'out_dtype': torch.float32}, 'plane'),
         ({'n_q': 65, 'n_k': 65, 'd': 16, 'dv': 16, 'contiguous': False}, 'plane'),  # model sites
-        ({'n_q': 100, 'n_k': 100}, 'mfma'),  # past one plane tile for 32-dim heads
+        ({'n_q': 100, 'n_k': 100}, 'tile'),  # past one plane tile for 32-dim heads
         ({'n_q': 100, 'n_k': 100, 'd': 16, 'dv': 16}, 'plane'),  # 16-dim heads: tiles of 128
-        ({'n_q': 65, 'n_k': 65, 'd': 64, 'dv': 64}, 'mfma'),
-        ({'n_q': 4096, 'n_k': 4096, 'd': 64, 'dv': 64}, 'mfma'),  # long key axis
+        ({'n_q': 200, 'n_k': 200, 'd': 16, 'dv': 16}, 'mfma'),  # 16-dim heads past 128 rows
+        ({'n_q': 65, 'n_k': 65, 'd': 64, 'dv': 64}, 'tile'),
+        ({'n_q': 4096, 'n_k': 4096, 'd': 64, 'dv': 64}, 'tile'),  # long key axis
+        ({'n_q': 4096, 'n_k': 4096, 'd': 64, 'dv': 64, 'dtype': torch.float32}, 'mfma'),
         ({'n_q': 65, 'n_k': 65, 'd': 48, 'dv': 48}, 'generic'),  # no MFMA tile for 48 dims
         ({'n_q': 15, 'n_k': 65}, 'stream'),  # under one query tile: rows stream two key tiles
     ],

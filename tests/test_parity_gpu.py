@@ -9,6 +9,7 @@ fp32 result rounded once (test_operator_output_is_the_rounded_fp32_result).
 """
 
 import math
+import zlib
 
 import numpy as np
 import pytest
@@ -38,7 +39,7 @@ def _variants(q, k, v, scale, bias):
     scale4, bias4 = capi.broadcast_operands(q, k, scale, bias)
     out = torch.empty((*q.shape[:-1], v.shape[-1]), device='cuda')
     found = ['auto']
-    for name in ('generic', 'stream', 'mfma', 'plane'):
+    for name in ('generic', 'stream', 'mfma', 'plane', 'tile'):
         if capi.select_variant(capi.make_args(q, k, v, out, scale4, bias4, name)) > 0:
             found.append(name)
     return found
@@ -305,6 +306,62 @@ def test_two_byte_bias_planes_at_any_alignment(bias_dtype, n_q):
                                out_dtype=torch.float32, variant=variant)
             np.testing.assert_allclose(got.cpu().double().numpy(), want, err_msg=f'{variant} offset {offset}',
                                        **HALF_TOL)
+
+
+# Shapes that reach the 16-bit query-tile kernels: one plane tile per wave
+# (head dims 16 and 32, <= 80 rows) and streamed key tiles (more keys, or
+# 64-dim heads).
+HALF_KERNEL_SHAPES = {'plane16': (24, 70, 16), 'plane32': (40, 65, 32), 'tile32': (40, 200, 32),
+                      'tile64': (33, 130, 64)}
+
+
+def _half_case(case, n_q, n_k, dim, gen):
+    q = torch.randn(2, 2, n_q, dim, generator=gen)
+    k = torch.randn(2, 2, n_k, dim, generator=gen)
+    v = torch.randn(2, 2, n_k, dim, generator=gen)
+    scale, bias = torch.tensor(0.5 / dim), None
+    if case == 'far_points':
+        # Every key far from every query (gamma d of a few hundred), so the
+        # weights underflow unless each query's largest logit is subtracted;
+        # distances stay where fp32 resolves them to the tolerance.
+        q, k, scale = q * 3, k * 3, torch.tensor(0.3)
+    elif case == 'negative_scale':
+        scale = torch.tensor(-0.01)
+    elif case == 'zero_scale':
+        scale = torch.tensor(0.0)
+        bias = torch.randn(2, 1, 1, n_k, generator=gen)
+    elif case == 'fully_masked':
+        bias = torch.zeros(2, 1, 1, n_k)
+        bias[1] = -math.inf
+    elif case == 'one_live_key':
+        bias = torch.full((2, 1, 1, n_k), -math.inf)
+        bias[..., n_k // 2] = 0.0
+    elif case == 'large_biases':  # a per-key bias far above the distance term
+        bias = 40.0 * torch.randn(2, 2, 1, n_k, generator=gen)
+    elif case == 'ragged_mask':
+        bias = torch.zeros(2, 1, 1, n_k)
+        bias[0, ..., n_k // 3:] = -math.inf
+    return q, k, v, scale, bias
+
+
+@pytest.mark.parametrize('case', ['far_points', 'negative_scale', 'zero_scale', 'fully_masked', 'one_live_key',
+                                  'large_biases', 'ragged_mask'])
+@pytest.mark.parametrize('shape', sorted(HALF_KERNEL_SHAPES))
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16], ids=str)
+def test_16bit_edge_cases(case, shape, dtype):
+    """Edge cases through the 16-bit kernels, including their exact-maximum
+    passes (far queries, gamma < 0, biases, fully masked rows)."""
+    n_q, n_k, dim = HALF_KERNEL_SHAPES[shape]
+    gen = torch.Generator().manual_seed(zlib.crc32(f'{case}/{shape}'.encode()) % 1000)
+    q, k, v, scale, bias = _half_case(case, n_q, n_k, dim, gen)
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    want = oracle.expanded_fp64(q, k, v, scale, bias)
+    variants = _variants(q, k, v, scale, bias)
+    assert ('plane' if shape.startswith('plane') else 'tile') in variants, variants
+    for variant in variants:
+        print(f'case={case} shape={shape} dtype={dtype} variant={variant}', flush=True)
+        got = run(q, k, v, scale, bias, variant).double().numpy()
+        np.testing.assert_allclose(got, want, equal_nan=True, err_msg=variant, **HALF_TOL)
 
 
 def test_empty_key_set_gives_zeros():

@@ -43,7 +43,7 @@ using vectra::make_fast_div;
 using vectra::Problem;
 
 constexpr int kAbiMajor = 1;
-constexpr int kAbiMinor = 1;
+constexpr int kAbiMinor = 2;
 
 bool is_io_dtype(int32_t d) { return d == VECTRA_F32 || d == VECTRA_F16 || d == VECTRA_BF16; }
 bool is_any_dtype(int32_t d) { return is_io_dtype(d) || d == VECTRA_F64; }
@@ -89,7 +89,7 @@ int validate(const vectra_rbf_args* a) {
   if (a->batch < 0 || a->heads < 0 || a->n_q < 0 || a->n_k < 0 || a->head_dim < 0 ||
       a->value_dim < 0)
     return VECTRA_ERR_BAD_SHAPE;
-  if (a->variant < VECTRA_VARIANT_AUTO || a->variant > VECTRA_VARIANT_PLANE)
+  if (a->variant < VECTRA_VARIANT_AUTO || a->variant > VECTRA_VARIANT_TILE)
     return VECTRA_ERR_BAD_VARIANT;
   const int64_t rows = a->batch * a->heads * a->n_q;
   if (rows == 0 || a->value_dim == 0) return VECTRA_OK;  // nothing to read or write
@@ -183,15 +183,18 @@ int select_variant(const vectra_rbf_args* a) {
   const Problem p = make_problem(a);
   const bool mfma = vectra::mfma_supports(p, a->in_dtype, a->out_dtype);
   const bool plane = vectra::plane_supports(p, a->in_dtype, a->out_dtype);
+  const bool tile = vectra::tile_supports(p, a->in_dtype, a->out_dtype);
   switch (a->variant) {
     case VECTRA_VARIANT_GENERIC: return VECTRA_VARIANT_GENERIC;
     case VECTRA_VARIANT_STREAM: return stream_chunks(a) ? VECTRA_VARIANT_STREAM : -VECTRA_ERR_BAD_VARIANT;
     case VECTRA_VARIANT_MFMA: return mfma ? VECTRA_VARIANT_MFMA : -VECTRA_ERR_BAD_VARIANT;
     case VECTRA_VARIANT_PLANE: return plane ? VECTRA_VARIANT_PLANE : -VECTRA_ERR_BAD_VARIANT;
+    case VECTRA_VARIANT_TILE: return tile ? VECTRA_VARIANT_TILE : -VECTRA_ERR_BAD_VARIANT;
     default: break;
   }
   if (a->n_q >= kMfmaMinQueries) {
     if (plane) return VECTRA_VARIANT_PLANE;
+    if (tile) return VECTRA_VARIANT_TILE;
     if (mfma) return VECTRA_VARIANT_MFMA;
   }
   return stream_chunks(a) ? VECTRA_VARIANT_STREAM : VECTRA_VARIANT_GENERIC;
@@ -222,6 +225,9 @@ int vectra_rbf_attention_fwd(const vectra_rbf_args* a, vectra_stream_t stream) {
       break;
     case VECTRA_VARIANT_PLANE:
       err = vectra::launch_plane(p, a->in_dtype, a->out_dtype, s);
+      break;
+    case VECTRA_VARIANT_TILE:
+      err = vectra::launch_tile(p, a->in_dtype, a->out_dtype, s);
       break;
     default:
       err = vectra::launch_generic(p, a->in_dtype, a->out_dtype, s);

@@ -30,6 +30,12 @@ hipError_t launch_mfma(Problem& p, int in_dtype, int out_dtype, hipStream_t s);
 bool plane_supports(const Problem& p, int in_dtype, int out_dtype);
 hipError_t launch_plane(Problem& p, int in_dtype, int out_dtype, hipStream_t s);
 
+// Tile kernel (key tiles streamed through LDS, 32 query rows per wave):
+// bf16/fp16 inputs, output in the input dtype or fp32, D == Dv in
+// {32, 64, 128}, unit d stride, 16-byte-aligned rows.
+bool tile_supports(const Problem& p, int in_dtype, int out_dtype);
+hipError_t launch_tile(Problem& p, int in_dtype, int out_dtype, hipStream_t s);
+
 hipError_t launch_squared_norms(const void* x, int dtype, int64_t B, int64_t H, int64_t N,
                                 int64_t D, const int64_t* strides, float* out, hipStream_t s);
 

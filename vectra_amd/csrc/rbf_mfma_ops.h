@@ -64,6 +64,15 @@ struct MfmaOps<_Float16> {
   }
 };
 
+// Two fp32 values as one 32-bit word of two OutT (round to nearest even,
+// each value first materialised in fp32: see from_float).
+template <typename OutT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  asm volatile("" : "+v"(a), "+v"(b));
+  typedef OutT o2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, o2));
+}
+
 template <>
 struct MfmaOps<float> {
   static __device__ __forceinline__ f32x4 mma(float a, float b, f32x4 c) {

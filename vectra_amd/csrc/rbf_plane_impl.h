@@ -115,15 +115,6 @@ __device__ __forceinline__ f32x4 plane_qk(uint2 k, uint2 q, f32x4 c) {
   return MfmaOps<T>::pv(__builtin_bit_cast(Pv, k), __builtin_bit_cast(Pv, q), c);
 }
 
-// Two fp32 values as one 32-bit word of two OutT (round to nearest even,
-// each value first materialised in fp32: see from_float).
-template <typename OutT>
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  asm volatile("" : "+v"(a), "+v"(b));
-  typedef OutT o2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, o2));
-}
-
 template <typename T, int kD, int kKeys>
 struct PlaneGeo {
   static_assert(sizeof(T) == 2, "16-bit inputs");

@@ -1,0 +1,483 @@
+// Streamed key tiles for long key axes on gfx950 matrix cores: the kernel
+// template, instantiated per dtype pair in rbf_tile_<in>_<out>.hip.
+//
+// A work item is one (b, h) plane and a block of 16 * kCB * kWaves query
+// rows; a workgroup of kWaves waves streams the plane's keys through LDS in
+// tiles of kKeys, and every wave reduces 16 * kCB queries (kCB 16-column
+// blocks) against each tile:
+//
+//   S^T = K . Q^T     (16 keys x 16 queries per instruction, 32-deep steps)
+//   O^T = V^T . P^T   (16 value dims x 16 queries)
+//
+// with the lane layouts of rbf_mfma_ops.h.  A K fragment read from LDS feeds
+// the products of every query block of the wave, and so does a V^T fragment:
+// two blocks per wave halve the LDS traffic per product.
+//
+// Per-score arithmetic is one FMA, one exp2 and the 16-bit split of the
+// weight:
+//  * -|q|^2 / 2 is the accumulator the first product starts from (one value
+//    per query column), so S = q.k - |q|^2 / 2;
+//  * gamma |k|^2 / 2 and the key bias are folded per tile into one value per
+//    key, c_j = log2(e) bias_j - gamma log2(e) |k_j|^2 (-inf past Nk);
+//  * x = 2 gamma log2(e) S + c_j = log2(e) (-gamma d + bias_j);
+//  * the softmax sum comes from the second product: a row of ones in its A
+//    operand sums the same hi + lo weights the values are weighted by.
+// Without a bias and with gamma >= 0, x <= 0 (d >= 0 up to rounding), so
+// exp2(x) is used as the weight directly: one pass over the keys, no running
+// maximum and no rescaling.  If a query's weight sum then ends below the
+// range in which the 16-bit split is accurate (the query is far from every
+// key), and always with a bias or gamma < 0, the item is computed exactly:
+// one pass finds each query's largest logit, a second subtracts it.
+// Weights are fed to the second product as hi + lo 16-bit pairs (~2^-17 of
+// each weight).  The distance is not clamped at zero: where rounding makes
+// the expansion negative, -d and the reference's max(d, 0) = 0 are both
+// within the expansion's rounding error of the true distance.
+//
+// Scheduling: persistent workgroups take items in a fixed order.  With a
+// grid and an item count that are multiples of the 8 XCDs (workgroups are
+// dispatched round-robin over them), the items are ordered so that every
+// item of a plane runs on one XCD, whose L2 then serves the plane's K and V
+// to all of them.  K and V tiles are stored row-major in LDS, as loaded; the
+// A operand of O^T is read with gfx950's transposing LDS read.  Tiles are
+// double-buffered: while a tile is reduced the next one is in flight into
+// registers and is written to the other buffer afterwards, with one barrier
+// per tile.
+
+#pragma once
+
+#include <atomic>
+
+#include "rbf_common.h"
+#include "rbf_kernels.h"
+#include "rbf_mfma_ops.h"
+
+namespace vectra {
+
+template <typename T, int kD, int kKeys, int kWaves, int kCB>
+struct TileGeo {
+  static_assert(sizeof(T) == 2, "16-bit inputs");
+  static_assert(kD % 32 == 0 && kKeys % 32 == 0, "whole 32-deep steps and key pairs");
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kQRows = 16 * kCB * kWaves;  // query rows per item
+  static constexpr int kKSteps = kD / 32;     // 32-deep steps of S^T
+  static constexpr int kPairs = kKeys / 32;   // 32-key steps of O^T
+  static constexpr int kDTiles = kD / 16;
+  static constexpr int kChunks = kD / 8;  // 16-byte chunks per K or V row
+  // K and V are stored row-major, as loaded.  K rows: a multiple of 8
+  // elements and an odd multiple of 16 bytes, so the 16 rows one 16-byte
+  // operand read touches start in distinct bank groups.  V rows: an odd
+  // multiple of 32 bytes, so the 4 x 32-byte row pieces of one transposing
+  // read (8 rows per 256 bytes of banks) do not collide.
+  static constexpr int kKStride = kD + 8;
+  static constexpr int kVStride = kD + 16;
+  static constexpr int kKBytes = kKeys * kKStride * 2;
+  static constexpr int kVBytes = kKeys * kVStride * 2;
+  static constexpr int kBufBytes = kKBytes + kVBytes + kKeys * 4;  // + c_j
+  static constexpr int kSlots = (kKeys * kChunks + kThreads - 1) / kThreads;
+  static constexpr bool kFull = kSlots * kThreads == kKeys * kChunks;
+};
+
+// Registers holding one tile's loads.  Slot s of a thread is chunk
+// slot % kChunks of key slot / kChunks (slot = tid + s * threads), of K and
+// of V; the thread holding chunk 0 of a key also loads its bias.
+template <typename T, int kD, int kKeys, int kWaves, int kCB>
+struct TileStage {
+  using G = TileGeo<T, kD, kKeys, kWaves, kCB>;
+  uint4 k[G::kSlots];
+  uint4 v[G::kSlots];
+  uint32_t bias[G::kSlots];
+  uint32_t bias_misalign;
+};
+
+// The 4 16-bit elements ds_read_b64_tr_b16 returns (see the A operand of
+// O^T in rbf_tile_kernel).
+typedef short tile_v4s __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const void* p) {
+  // A C-style cast converts the generic pointer to the LDS address space.
+  const tile_v4s r =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tile_v4s*)(const_cast<void*>(p)));
+  return __builtin_bit_cast(uint2, r);
+}
+
+// Pass kinds of one item.
+enum TilePass : int { kPassSum = 0, kPassMax = 1, kPassShifted = 2 };
+
+// Three waves per SIMD (at most 168 VGPRs) measured fastest for head dims
+// up to 64; 128-dim heads keep two.
+template <typename T, typename OutT, int kD, int kKeys, int kWaves, int kCB>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kD <= 64 ? 3 : 2))) void
+rbf_tile_kernel(Problem p, int32_t q_blocks) {
+  using G = TileGeo<T, kD, kKeys, kWaves, kCB>;
+  using Ops = MfmaOps<T>;
+  using Stage = TileStage<T, kD, kKeys, kWaves, kCB>;
+  using Qk = typename Ops::Qk;
+  constexpr int kThreads = G::kThreads;
+  constexpr int kChunks = G::kChunks;
+  constexpr int kKSteps = G::kKSteps;
+  constexpr int kDTiles = G::kDTiles;
+  constexpr uint32_t kOutSize = sizeof(OutT);
+  // Weight sums that need no exact pass: bf16 weights are at most 1 and the
+  // largest one at least 2^-32 / Nk, far inside the normal range, where the
+  // hi + lo split keeps 2^-17 of it; fp16's subnormal steps of 2^-24 stay
+  // below 2^-21 of a sum of at least 2^-3.
+  constexpr bool kBf16 = __is_same(T, __bf16);
+  constexpr float kSumLo = kBf16 ? 0x1p-32f : 0x1p-3f;
+
+  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ int32_t exact_flag[2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+
+  const int32_t n_q = static_cast<int32_t>(p.Nq);
+  const int32_t n_k = static_cast<int32_t>(p.Nk);
+  const int32_t items = static_cast<int32_t>(p.B * p.H) * q_blocks;
+  const int32_t tiles = (n_k + kKeys - 1) / kKeys;
+  const bool has_bias = p.bias != nullptr;
+  const int32_t bias_esize = p.bias_dtype == VECTRA_F32 ? 4 : 2;
+  const uint32_t q_row_bytes = static_cast<uint32_t>(p.sq[2]) * 2u;
+  const uint32_t k_row_bytes = static_cast<uint32_t>(p.sk[2]) * 2u;
+  const uint32_t v_row_bytes = static_cast<uint32_t>(p.sv[2]) * 2u;
+  const uint32_t o_row = static_cast<uint32_t>(p.so[2]);
+  const uint32_t o_dim = static_cast<uint32_t>(p.so[3]);
+  const bool out_vec = p.so[3] == 1 && p.so[2] % 4 == 0 && p.so[1] % 4 == 0 && p.so[0] % 4 == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.out) & 15u) == 0;
+  // XCD-local item order (see the header comment); a bijection of [0, items).
+  const int32_t grid = static_cast<int32_t>(gridDim.x);
+  const bool xcd_order = grid % 8 == 0 && items % 8 == 0;
+  const int32_t per_xcd = items / 8;
+  auto item_of = [&](int32_t slot) { return xcd_order ? (slot & 7) * per_xcd + (slot >> 3) : slot; };
+
+  struct Coords {
+    int32_t b, h, qb;
+  };
+  auto coords = [&](int32_t item) {
+    Coords c;
+    const int32_t bh = static_cast<int32_t>(fast_div(static_cast<uint32_t>(item), p.nq_mul, p.nq_shift));
+    c.qb = item - bh * q_blocks;
+    c.b = static_cast<int32_t>(fast_div(static_cast<uint32_t>(bh), p.h_mul, p.h_shift));
+    c.h = bh - c.b * static_cast<int32_t>(p.H);
+    return c;
+  };
+
+  // Issues the loads of tile `tile` of the plane of `c` into `st`.  Rows past
+  // Nk read row Nk - 1 (in bounds) and are masked when published.
+  auto issue = [&](Stage& st, const Coords& c, int32_t tile) {
+    const char* kp = static_cast<const char*>(p.k) + (c.b * p.sk[0] + c.h * p.sk[1]) * 2;
+    const char* vp = static_cast<const char*>(p.v) + (c.b * p.sv[0] + c.h * p.sv[1]) * 2;
+    const int32_t j0 = tile * kKeys;
+#pragma unroll
+    for (int s = 0; s < G::kSlots; ++s) {
+      const int slot = tid + s * kThreads;
+      if (G::kFull || slot < kKeys * kChunks) {
+        const uint32_t row = static_cast<uint32_t>(min(j0 + slot / kChunks, n_k - 1));
+        const uint32_t chunk_off = static_cast<uint32_t>(slot % kChunks) * 16u;
+        st.k[s] = load16_stream(kp + row * k_row_bytes + chunk_off);
+        st.v[s] = load16_stream(vp + row * v_row_bytes + chunk_off);
+      }
+    }
+    if (has_bias) {
+      const char* bp = static_cast<const char*>(p.bias) + (c.b * p.sbb + c.h * p.sbh) * bias_esize;
+      st.bias_misalign = base_misalign(bp);
+#pragma unroll
+      for (int s = 0; s < G::kSlots; ++s) {
+        const int slot = tid + s * kThreads;
+        const uint32_t key = static_cast<uint32_t>(min(j0 + slot / kChunks, n_k - 1));
+        st.bias[s] = load_raw_scalar32(bp, st.bias_misalign, key * static_cast<uint32_t>(p.sbn), p.bias_dtype).word;
+      }
+    }
+  };
+
+  // Writes a staged tile into LDS buffer `buf`: K and V rows, and per key
+  // c_j = log2(e) bias_j - coef |k_j|^2 / 2 (-inf past Nk).
+  auto publish = [&](const Stage& st, int32_t tile, int buf, float coef) {
+    const int32_t j0 = tile * kKeys;
+    T* kl = reinterpret_cast<T*>(lds + buf * G::kBufBytes);
+    T* vl = reinterpret_cast<T*>(lds + buf * G::kBufBytes + G::kKBytes);
+    float* cl = reinterpret_cast<float*>(lds + buf * G::kBufBytes + G::kKBytes + G::kVBytes);
+#pragma unroll
+    for (int s = 0; s < G::kSlots; ++s) {
+      const int slot = tid + s * kThreads;
+      if (G::kFull || slot < kKeys * kChunks) {
+        const int key = slot / kChunks;
+        const int d0 = (slot % kChunks) * 8;
+        *reinterpret_cast<uint4*>(kl + key * G::kKStride + d0) = st.k[s];
+        // Rows past Nk are zeroed in V: their weight is 0, and 0 times a
+        // non-finite copy would not be.
+        *reinterpret_cast<uint4*>(vl + key * G::kVStride + d0) =
+            j0 + key < n_k ? st.v[s] : make_uint4(0, 0, 0, 0);
+        // |k|^2 over the chunks of the row (kChunks adjacent lanes).
+        const float sq = reduce_low<kChunks>(dot_chunk<T>(st.k[s], st.k[s], 0.f), OpSum());
+        if (slot % kChunks == 0) {
+          float bias = 0.f;
+          if (has_bias) {
+            const uint32_t j = static_cast<uint32_t>(min(j0 + key, n_k - 1));
+            const uint32_t bytes = j * static_cast<uint32_t>(p.sbn) * bias_esize + st.bias_misalign;
+            bias = decode_raw_scalar(RawScalar{st.bias[s], (bytes & 2u) * 8u}, p.bias_dtype) * kLog2e;
+          }
+          cl[key] = j0 + key < n_k ? fmaf(-0.5f * coef, sq, bias) : -INFINITY;
+        }
+      }
+    }
+  };
+
+  const uint32_t one = Ops::kOnePair;
+  const Qk ones8 = __builtin_bit_cast(Qk, make_uint4(one, one, one, one));
+
+  // Per-wave query state of the current item: the B operands of the two
+  // 16-column blocks, -|q|^2 / 2, and the accumulators.
+  uint4 qf[kCB][kKSteps];
+  f32x4 q_half[kCB];  // -|q|^2 / 2 in every row: the first product's accumulator
+  float row_max[kCB];
+  f32x4 acc[kCB][kDTiles];
+  f32x4 total[kCB];
+
+  // Reduces tile `buf` for the wave's 32 queries.
+  auto compute = [&](int buf, float coef, int kind) {
+    const T* kl = reinterpret_cast<const T*>(lds + buf * G::kBufBytes);
+    const T* vl = reinterpret_cast<const T*>(lds + buf * G::kBufBytes + G::kKBytes);
+    const float* cl = reinterpret_cast<const float*>(lds + buf * G::kBufBytes + G::kKBytes + G::kVBytes);
+#pragma unroll
+    for (int kp = 0; kp < G::kPairs; ++kp) {
+      // S^T for key blocks 2kp, 2kp + 1 and both query blocks.
+      f32x4 s[kCB][2];
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+#pragma unroll
+        for (int ks = 0; ks < kKSteps; ++ks) {
+          const Qk a = *reinterpret_cast<const Qk*>(kl + (32 * kp + 16 * hb + col) * G::kKStride + 32 * ks + 8 * grp);
+#pragma unroll
+          for (int cb = 0; cb < kCB; ++cb)
+            s[cb][hb] = Ops::qk(a, __builtin_bit_cast(Qk, qf[cb][ks]), ks == 0 ? q_half[cb] : s[cb][hb]);
+        }
+      }
+      float x[kCB][2][4];
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        const float4 c = *reinterpret_cast<const float4*>(cl + 32 * kp + 16 * hb + 4 * grp);
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb) {
+          x[cb][hb][0] = fmaf(coef, s[cb][hb][0], c.x);
+          x[cb][hb][1] = fmaf(coef, s[cb][hb][1], c.y);
+          x[cb][hb][2] = fmaf(coef, s[cb][hb][2], c.z);
+          x[cb][hb][3] = fmaf(coef, s[cb][hb][3], c.w);
+        }
+      }
+      if (kind == kPassMax) {
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+          for (int hb = 0; hb < 2; ++hb)
+            row_max[cb] = fmaxf(row_max[cb], fmaxf(fmaxf(x[cb][hb][0], x[cb][hb][1]), fmaxf(x[cb][hb][2], x[cb][hb][3])));
+        continue;
+      }
+      Qk p_hi[kCB], p_lo[kCB];
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) {
+        const float shift = kind == kPassShifted ? row_max[cb] : 0.f;
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+          float w[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) w[r] = __builtin_amdgcn_exp2f(x[cb][hb][r] - shift);
+          Ops::split2(w[0], w[1], hi[2 * hb], lo[2 * hb]);
+          Ops::split2(w[2], w[3], hi[2 * hb + 1], lo[2 * hb + 1]);
+        }
+        p_hi[cb] = __builtin_bit_cast(Qk, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+        p_lo[cb] = __builtin_bit_cast(Qk, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+      }
+#pragma unroll
+      for (int u = 0; u < kDTiles; ++u) {
+        // A operand of O^T: lane (dim 16u + col, group g) gets keys
+        // 32kp + 4g + 0..3 and 32kp + 16 + 4g + 0..3 of that dim.  Within a
+        // group of 16 lanes, ds_read_b64_tr_b16 gives lane i element i % 4
+        // of the 4-element pieces addressed by lanes i / 4, 4 + i / 4,
+        // 8 + i / 4 and 12 + i / 4, so lane i addresses key row
+        // 32kp + 4g + i / 4 (+16), dims 16u + 4 (i % 4) .. +3.
+        const T* va = vl + (32 * kp + 4 * grp + col / 4) * G::kVStride + 16 * u + 4 * (col % 4);
+        const uint2 a0 = lds_read_tr16(va);
+        const uint2 a1 = lds_read_tr16(va + 16 * G::kVStride);
+        const Qk a = __builtin_bit_cast(Qk, make_uint4(a0.x, a0.y, a1.x, a1.y));
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb) {
+          acc[cb][u] = Ops::qk(a, p_hi[cb], acc[cb][u]);
+          acc[cb][u] = Ops::qk(a, p_lo[cb], acc[cb][u]);
+        }
+      }
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) {
+        total[cb] = Ops::qk(ones8, p_hi[cb], total[cb]);
+        total[cb] = Ops::qk(ones8, p_lo[cb], total[cb]);
+      }
+      // One key pair at a time: keeps the next pair's operands from being
+      // hoisted over this pair's products (register pressure).
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // One pass of an item over every key tile (double-buffered, one barrier
+  // per tile).  Every wave of the workgroup runs it.
+  Stage st;
+  auto run_pass = [&](const Coords& c, float coef, int kind) {
+    if (kind != kPassMax) {
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) {
+#pragma unroll
+        for (int u = 0; u < kDTiles; ++u) acc[cb][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        total[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    issue(st, c, 0);
+    publish(st, 0, 0, coef);
+    __syncthreads();
+    if (tiles > 1) issue(st, c, 1);
+    for (int32_t t = 0; t < tiles; ++t) {
+      compute(t & 1, coef, kind);
+      if (t + 1 < tiles) publish(st, t + 1, (t + 1) & 1, coef);
+      __syncthreads();
+      if (t + 2 < tiles) issue(st, c, t + 2);
+    }
+  };
+
+  int32_t parity = 0;
+  for (int32_t slot = static_cast<int32_t>(blockIdx.x); slot < items; slot += grid, parity ^= 1) {
+    const Coords c = coords(item_of(slot));
+    if (tid == 0) exact_flag[parity] = 0;  // read after the first barrier of this item
+    const float coef = 2.f * kLog2e * load_any(p.scale, c.b * p.ssb + c.h * p.ssh, p.scale_dtype);
+    // Query rows of this wave: item rows (wave * kCB + cb) * 16 + col (rows
+    // past Nq read row Nq - 1 and are not stored).
+    {
+      const char* qp = static_cast<const char*>(p.q) + (c.b * p.sq[0] + c.h * p.sq[1]) * 2;
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) {
+        const uint32_t row = static_cast<uint32_t>(min(c.qb * G::kQRows + (wave * kCB + cb) * 16 + col, n_q - 1));
+        float sq = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < kKSteps; ++ks) {
+          qf[cb][ks] = load16(qp + row * q_row_bytes + static_cast<uint32_t>(64 * ks + 16 * grp));
+          sq = dot_chunk<T>(qf[cb][ks], qf[cb][ks], sq);
+        }
+        const float h = -0.5f * allreduce_bit32(allreduce_bit16(sq, OpSum()), OpSum());
+        q_half[cb] = f32x4{h, h, h, h};
+      }
+    }
+    // The single pass needs x <= 0: no bias and gamma >= 0.
+    bool exact = has_bias || !(coef >= 0.f);
+    if (!exact) {
+      run_pass(c, coef, kPassSum);
+      // A weight sum below the accurate range (or NaN) anywhere in the
+      // workgroup sends the item to the exact passes.
+      bool low = false;
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) low = low || !(total[cb][0] >= kSumLo);
+      if (__builtin_amdgcn_ballot_w64(low) && lane == 0) exact_flag[parity] = 1;
+      __syncthreads();
+      exact = exact_flag[parity] != 0;
+    }
+    if (exact) {
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) row_max[cb] = -INFINITY;
+      run_pass(c, coef, kPassMax);
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) {
+        const float m = allreduce_bit32(allreduce_bit16(row_max[cb], OpMax()), OpMax());
+        row_max[cb] = m == -INFINITY ? 0.f : m;  // every key masked: the row ends as NaN
+      }
+      run_pass(c, coef, kPassShifted);
+    }
+
+    // Store: every row of the ones product holds the query's weight sum; a
+    // fully masked row has sum 0 and ends as 0 * inf = NaN.
+    char* out_plane = static_cast<char*>(p.out) + (c.b * p.so[0] + c.h * p.so[1]) * static_cast<int64_t>(kOutSize);
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb) {
+      const int32_t q_row = c.qb * G::kQRows + (wave * kCB + cb) * 16 + col;
+      if (q_row < n_q) {
+        const float inv = __builtin_amdgcn_rcpf(total[cb][0]);
+        const uint32_t row_off = static_cast<uint32_t>(q_row) * o_row;
+#pragma unroll
+        for (int u = 0; u < kDTiles; ++u) {
+          const uint32_t off = (row_off + static_cast<uint32_t>(16 * u + 4 * grp) * o_dim) * kOutSize;
+          const float y0 = acc[cb][u][0] * inv, y1 = acc[cb][u][1] * inv;
+          const float y2 = acc[cb][u][2] * inv, y3 = acc[cb][u][3] * inv;
+          if constexpr (kOutSize == 4) {
+            if (out_vec) {
+              *reinterpret_cast<float4*>(out_plane + off) = make_float4(y0, y1, y2, y3);
+            } else {
+              const float ys[4] = {y0, y1, y2, y3};
+#pragma unroll
+              for (int r = 0; r < 4; ++r) *reinterpret_cast<float*>(out_plane + off + r * o_dim * 4u) = ys[r];
+            }
+          } else {
+            const uint32_t w01 = pack2<OutT>(y0, y1), w23 = pack2<OutT>(y2, y3);
+            if (out_vec) {
+              *reinterpret_cast<uint2*>(out_plane + off) = make_uint2(w01, w23);
+            } else {
+              const uint16_t hs[4] = {static_cast<uint16_t>(w01), static_cast<uint16_t>(w01 >> 16),
+                                      static_cast<uint16_t>(w23), static_cast<uint16_t>(w23 >> 16)};
+#pragma unroll
+              for (int r = 0; r < 4; ++r) *reinterpret_cast<uint16_t*>(out_plane + off + r * o_dim * 2u) = hs[r];
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------- host
+
+template <typename T, typename OutT, int kD, int kKeys, int kWaves, int kCB>
+int tile_resident_blocks() {
+  static std::atomic<int> cached{0};
+  int n = cached.load(std::memory_order_relaxed);
+  if (n == 0) {
+    using G = TileGeo<T, kD, kKeys, kWaves, kCB>;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void*>(&rbf_tile_kernel<T, OutT, kD, kKeys, kWaves, kCB>), 64 * kWaves,
+            2 * G::kBufBytes) != hipSuccess ||
+        n < 1)
+      n = 1;
+    cached.store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+template <typename T, typename OutT, int kD, int kKeys, int kWaves, int kCB>
+hipError_t launch_tile_k(Problem& p, hipStream_t s) {
+  using G = TileGeo<T, kD, kKeys, kWaves, kCB>;
+  const int32_t q_blocks = static_cast<int32_t>((p.Nq + G::kQRows - 1) / G::kQRows);
+  const int64_t items = p.B * p.H * q_blocks;
+  int64_t blocks = static_cast<int64_t>(tile_resident_blocks<T, OutT, kD, kKeys, kWaves, kCB>()) *
+                   (p.compute_units > 0 ? p.compute_units : 1);
+  if (blocks > items) blocks = items;
+  if (blocks >= 8) blocks -= blocks % 8;  // whole XCD rounds (see the kernel)
+  if (items + blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  Problem k = p;  // the kernel divides work items by q_blocks with the Nq slots
+  make_fast_div(q_blocks, &k.nq_mul, &k.nq_shift);
+  int32_t qb = q_blocks;
+  void* args[] = {&k, &qb};
+  return hipLaunchKernel(reinterpret_cast<const void*>(&rbf_tile_kernel<T, OutT, kD, kKeys, kWaves, kCB>),
+                         dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves), args, 2 * G::kBufBytes, s);
+}
+
+template <typename T, typename OutT>
+hipError_t launch_tile_t(Problem& p, hipStream_t s) {
+  switch (p.D) {
+    case 32: return launch_tile_k<T, OutT, 32, 64, 4, 2>(p, s);
+    case 64: return launch_tile_k<T, OutT, 64, 64, 4, 2>(p, s);
+    case 128: return launch_tile_k<T, OutT, 128, 32, 4, 2>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_tile_bf16_bf16(Problem& p, hipStream_t s);
+hipError_t launch_tile_bf16_f32(Problem& p, hipStream_t s);
+hipError_t launch_tile_f16_f16(Problem& p, hipStream_t s);
+hipError_t launch_tile_f16_f32(Problem& p, hipStream_t s);
+
+}  // namespace vectra

@@ -27,7 +27,7 @@ ERR_LAUNCH = 6
 ERR_BAD_VARIANT = 7
 
 # Kernel variants.
-VARIANTS = {'auto': 0, 'generic': 1, 'stream': 2, 'mfma': 3, 'plane': 4}
+VARIANTS = {'auto': 0, 'generic': 1, 'stream': 2, 'mfma': 3, 'plane': 4, 'tile': 5}
 VARIANT_NAMES = {v: k for k, v in VARIANTS.items()}
 
 # Exported functions, as declared in include/vectra_rbf.h.
