@@ -145,3 +145,23 @@ def test_empty_key_set_gives_zeros_like_eager():
     out = torch.ops.vectra.rbf_attention(q, k, v, torch.tensor(0.1))
     assert torch.equal(out, oracle.eager_fp32(q, k, v, torch.tensor(0.1)))
     assert torch.equal(out, torch.zeros(1, 2, 3, 5))
+
+
+def test_non_finite_values_in_masked_rows_propagate_on_the_cpu():
+    """The CPU implementation keeps eager's NaN propagation through masked
+    keys: NaN in a masked K row makes the query row NaN, inf or NaN in a
+    masked V row makes that value dim NaN."""
+    gen = torch.Generator().manual_seed(11)
+    q = torch.randn(3, 2, 5, 16, generator=gen)
+    k = torch.randn(3, 2, 40, 16, generator=gen)
+    v = torch.randn(3, 2, 40, 16, generator=gen)
+    bias = torch.zeros(3, 1, 1, 40)
+    bias[..., 20:] = -math.inf
+    k[0, 1, 39, 3] = math.nan
+    v[1, 0, 38, 5] = math.inf
+    v[1, 1, 20, 7] = math.nan
+    scale = torch.tensor(0.05)
+    want = oracle.expanded_fp64(q, k, v, scale, bias)
+    assert np.isnan(want[0, 1]).all() and np.isnan(want[1, 0, :, 5]).all()
+    got = torch.ops.vectra.rbf_attention(q, k, v, scale, bias).double().numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6, equal_nan=True)

@@ -237,6 +237,41 @@ def test_fully_masked_rows_are_nan(n_k):
         assert torch.isnan(out[1]).all() and torch.isfinite(out[0]).all(), variant
 
 
+# (Nq, Nk, D): the stream kernel (one query row), the plane kernel (both axes
+# one tile, D = 32 and 16), streamed key tiles; fp32 reaches the MFMA kernel.
+MASKED_ROW_SHAPES = [(1, 64, 32), (65, 65, 32), (24, 70, 16), (40, 200, 32)]
+
+
+@pytest.mark.parametrize('shape', MASKED_ROW_SHAPES, ids=str)
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32], ids=str)
+def test_non_finite_values_in_masked_rows_propagate(shape, dtype):
+    """A key masked by a -inf bias still reaches the output through 0 * x:
+    NaN in its K row makes every output of the query row NaN, and inf or NaN
+    in its V row makes that value dim NaN, as in the eager chain.  Kernels
+    that skip the products of masked key blocks must keep these."""
+    n_q, n_k, dim = shape
+    gen = torch.Generator().manual_seed(11)
+    q = torch.randn(3, 2, n_q, dim, generator=gen)
+    k = torch.randn(3, 2, n_k, dim, generator=gen)
+    v = torch.randn(3, 2, n_k, dim, generator=gen)
+    bias = torch.zeros(3, 1, 1, n_k)
+    bias[..., n_k // 2:] = -math.inf  # a masked suffix, as padding gives
+    k[0, 1, n_k - 1, 3] = math.nan
+    v[1, 0, n_k - 2, 5] = math.inf
+    v[1, 1, n_k // 2, 7] = math.nan
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    scale = torch.tensor(0.05)
+    want = oracle.expanded_fp64(q, k, v, scale, bias)
+    assert np.isnan(want[0, 1]).all() and np.isfinite(want[0, 0]).all() and np.isfinite(want[2]).all()
+    assert np.isnan(want[1, 0, :, 5]).all() and np.isnan(want[1, 1, :, 7]).all()
+    assert np.isfinite(np.delete(want[1, 0], 5, axis=-1)).all()
+    tol = FP32_TOL if dtype == torch.float32 else HALF_TOL
+    for variant in _variants(q, k, v, scale, bias):
+        print(f'shape={shape} dtype={dtype} variant={variant}', flush=True)
+        got = run(q, k, v, scale, bias, variant).double().numpy()
+        np.testing.assert_allclose(got, want, equal_nan=True, err_msg=variant, **tol)
+
+
 def test_far_points_do_not_underflow():
     gen = torch.Generator().manual_seed(6)
     q = torch.randn(2, 2, 10, 32, generator=gen) * 20

@@ -190,10 +190,16 @@ void rbf_stream_kernel(Problem p) {
     const char* vp = reinterpret_cast<const char*>(p.v) + (c.b * p.sv[0] + c.h * p.sv[1]) * sizeof(T);
     // With one tile per row (Nk <= 64) the offsets are loop invariant.
     const Offsets o = (kSingleTile || tile == 0) ? first : tile_offsets(tile);
-#pragma unroll
-    for (int s = 0; s < kPasses; ++s) slot.k[s] = load16_stream(kp + o.k[s]);
-#pragma unroll
-    for (int s = 0; s < kPasses; ++s) slot.v[s] = load16_stream(vp + o.v[s]);
+    // Issue order is use order: vector loads complete in order, so q, the
+    // coefficient and the biases go first and K before V; the scores are
+    // then computed while V is still arriving, and only the value product
+    // waits for the last bytes.
+    if (tile == 0) {
+      const char* qp = reinterpret_cast<const char*>(p.q) +
+                       (c.b * p.sq[0] + c.h * p.sq[1] + c.i * p.sq[2]) * sizeof(T);
+      slot.q = load16(qp + chunk_bytes);
+      slot.scale = load_raw_scalar(p.scale, c.b * p.ssb + c.h * p.ssh, p.scale_dtype);
+    }
     if (has_bias) {
       const char* bp = reinterpret_cast<const char*>(p.bias) +
                        (c.b * p.sbb + c.h * p.sbh) * bias_esize;
@@ -202,12 +208,13 @@ void rbf_stream_kernel(Problem p) {
       for (int s = 0; s < kPasses; ++s)
         slot.bias[s] = load_raw_scalar32(bp, slot.bias_misalign, o.bias[s], p.bias_dtype).word;
     }
-    if (tile == 0) {
-      const char* qp = reinterpret_cast<const char*>(p.q) +
-                       (c.b * p.sq[0] + c.h * p.sq[1] + c.i * p.sq[2]) * sizeof(T);
-      slot.q = load16(qp + chunk_bytes);
-      slot.scale = load_raw_scalar(p.scale, c.b * p.ssb + c.h * p.ssh, p.scale_dtype);
-    }
+#pragma unroll
+    for (int s = 0; s < kPasses; ++s) slot.k[s] = load16_stream(kp + o.k[s]);
+#pragma unroll
+    for (int s = 0; s < kPasses; ++s) slot.v[s] = load16_stream(vp + o.v[s]);
+    // Nothing that waits for a load may be scheduled among them (a wait for
+    // q or a bias there would hold back the V loads by a memory latency).
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // Per-row running state.
@@ -235,7 +242,7 @@ void rbf_stream_kernel(Problem p) {
       live[s] = j < n_k;
       const float dot = reduce_low<kChunks>(dot_chunk<T>(q_raw, slot.k[s], 0.f), OpSum());
       const float k_norm = reduce_low<kChunks>(dot_chunk<T>(slot.k[s], slot.k[s], 0.f), OpSum());
-      const float dist = fmaxf((q_norm + k_norm) - 2.f * dot, 0.f);
+      const float dist = clamp_distance((q_norm + k_norm) - 2.f * dot);
       float x = neg_scale * dist;
       if (has_bias) {
         // Position of a 2-byte bias inside its word, from the key index
@@ -404,7 +411,7 @@ __global__ __launch_bounds__(256) void rbf_generic_kernel(Problem p) {
         dot += qd * kd;
         k_norm += kd * kd;
       }
-      const float dist = fmaxf((q_norm + k_norm) - 2.f * dot, 0.f);
+      const float dist = clamp_distance((q_norm + k_norm) - 2.f * dot);
       logit = neg_scale * dist;
       if (has_bias) logit += load_any(p.bias, bias_base + j * p.sbn, p.bias_dtype);
     }

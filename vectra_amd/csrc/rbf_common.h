@@ -49,6 +49,14 @@ __device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
+// max(d, 0) for an expanded squared distance, keeping NaN (one
+// v_maximum3_f32): a NaN in q or k must reach the softmax, where it makes the
+// row NaN as the eager chain's (q - k)^2 does, even for a masked key.
+// fmaxf(NaN, 0) would return 0.
+__device__ __forceinline__ float clamp_distance(float d) {
+  return __builtin_elementwise_maximum(d, 0.f);
+}
+
 // Loads element i of a buffer whose dtype is only known at run time
 // (scale and key_bias accept any floating dtype) and converts it to fp32.
 __device__ __forceinline__ float load_any(const void* p, int64_t i, int32_t dtype) {

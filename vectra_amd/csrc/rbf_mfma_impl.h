@@ -356,8 +356,10 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
       }
       const float4 bias = *reinterpret_cast<const float4*>(bias_lds + 16 * t + 4 * grp);
       const float bv[4] = {bias.x, bias.y, bias.z, bias.w};
+      // min(-d/2, 0) keeping NaN (v_minimum3_f32), so a NaN in q or k makes
+      // the row NaN as in the eager chain, even for a masked key.
 #pragma unroll
-      for (int r = 0; r < 4; ++r) logit[t][r] = fmaf(coef, fminf(sc[r], 0.f), bv[r]);
+      for (int r = 0; r < 4; ++r) logit[t][r] = fmaf(coef, __builtin_elementwise_minimum(sc[r], 0.f), bv[r]);
       tile_max = fmaxf(tile_max, fmaxf(fmaxf(logit[t][0], logit[t][1]), fmaxf(logit[t][2], logit[t][3])));
     }
     tile_max = allreduce_bit32(allreduce_bit16(tile_max, OpMax()), OpMax());
