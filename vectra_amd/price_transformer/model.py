@@ -5,9 +5,10 @@ Transformer blocks with spatial (RBF) attention mix them, and the subject
 token is read out as a correction to the comparables' mean log price.  Same
 architecture and forward semantics as the reference's
 models/price_transformer/model.py:39-282; trimming comparables to the search
-radius (with a nearest-neighbour fallback) is a torch.cond, so TorchDynamo
-captures the forward pass as a single graph and every attention site stays
-visible to the rewrite.
+radius (with a nearest-neighbour fallback) is branch-free tensor code, so
+TorchDynamo captures the forward pass as a single graph, every attention
+site stays visible to the rewrite, and a forward pass never waits for the
+GPU.
 """
 
 import dataclasses
@@ -64,20 +65,20 @@ class PricingInputs(typing.NamedTuple):
 def trim_to_radius(distance_km, radius_km, valid, min_keep: int) -> torch.Tensor:
     """Comparables inside the radius; rows with none keep their `min_keep` nearest.
 
-    A data-dependent choice, so a torch.cond rather than a Python branch.
+    The reference (models/price_transformer/model.py:96-138) picks between an
+    inside-only branch and this nearest-neighbour fallback with a torch.cond
+    on "every row has a comparable inside".  Both give the same mask on every
+    row the inside-only branch covers, so here the fallback is always taken
+    and selected per row: the same mask with no data-dependent branch.  The
+    cond's predicate is a device-to-host read on every forward pass, which
+    stalls the host until the GPU has caught up, so the model could not be
+    launched ahead of the GPU, overlapped with the next batch's copy, or
+    captured in a HIP graph.
     """
-
-    def inside_only(distance, radius, mask):
-        return mask & (distance <= radius.unsqueeze(-1))
-
-    def nearest_fallback(distance, radius, mask):
-        inside = mask & (distance <= radius.unsqueeze(-1))
-        nearest = distance.masked_fill(~mask, float('inf')).topk(min_keep, dim=-1, largest=False).indices
-        fallback = torch.zeros_like(mask).scatter(-1, nearest, True) & mask
-        return torch.where(inside.any(-1, keepdim=True), inside, fallback)
-
-    covered = (valid & (distance_km <= radius_km.unsqueeze(-1))).any(-1).all()
-    return torch.cond(covered, inside_only, nearest_fallback, (distance_km, radius_km, valid))
+    inside = valid & (distance_km <= radius_km.unsqueeze(-1))
+    nearest = distance_km.masked_fill(~valid, float('inf')).topk(min_keep, dim=-1, largest=False).indices
+    fallback = torch.zeros_like(valid).scatter(-1, nearest, True) & valid
+    return torch.where(inside.any(-1, keepdim=True), inside, fallback)
 
 
 class Block(nn.Module):
