@@ -43,7 +43,8 @@
 // row ends as 0 * (1 / 0) = NaN, as eager softmax gives.
 //
 // Scheduling: the grid is persistent (as many one-wave workgroups as fit at
-// once); a wave takes planes blockIdx.x, blockIdx.x + gridDim.x, ...  Right
+// once); a wave takes slots blockIdx.x, blockIdx.x + gridDim.x, ..., each
+// slot mapped to a plane so that an XCD works on contiguous planes.  Right
 // after a plane's operands are in place (K in registers; V^T, the folded
 // biases and q in LDS) every load of the wave's next plane is issued into
 // registers, so its HBM latency overlaps the whole of this plane's products.
@@ -183,8 +184,21 @@ __global__ __launch_bounds__(64) void rbf_plane_kernel(Problem p) {
   const int grp = lane >> 4;
 
   const int32_t planes = static_cast<int32_t>(p.B * p.H);
-  int32_t plane = static_cast<int32_t>(blockIdx.x);
-  if (plane >= planes) return;  // one-wave workgroups: no barrier to miss
+  int32_t slot = static_cast<int32_t>(blockIdx.x);
+  if (slot >= planes) return;  // one-wave workgroups: no barrier to miss
+  // XCD-local plane order.  Workgroups are dispatched round-robin over the 8
+  // XCDs, so with a grid and a plane count that are multiples of 8, slot s
+  // runs on XCD s % 8; giving XCD x the contiguous planes x * planes / 8 ..
+  // puts the heads of one batch entry on one XCD at the same time.  Where
+  // q, k and v are head-transposed views of one projection (the model's
+  // sites), a cache line holds rows of several heads, and its L2 then
+  // fetches it from HBM once instead of once per XCD.  A bijection of
+  // [0, planes).
+  const int32_t grid = static_cast<int32_t>(gridDim.x);
+  const bool xcd_order = grid % 8 == 0 && planes % 8 == 0;
+  const int32_t per_xcd = planes / 8;
+  auto plane_of = [&](int32_t s) { return xcd_order ? (s & 7) * per_xcd + (s >> 3) : s; };
+  int32_t plane = plane_of(slot);
   const int32_t n_q = static_cast<int32_t>(p.Nq);
   const int32_t n_k = static_cast<int32_t>(p.Nk);
   const int32_t q_blocks = (n_q + 15) / 16;
@@ -467,12 +481,14 @@ __global__ __launch_bounds__(64) void rbf_plane_kernel(Problem p) {
     int32_t b, h;
     plane_bh(plane, b, h);
     char* out_plane = static_cast<char*>(p.out) + (b * p.so[0] + h * p.so[1]) * static_cast<int64_t>(kOutSize);
-    const int32_t next = plane + static_cast<int32_t>(gridDim.x);
-    const bool more = next < planes;
+    const int32_t next_slot = slot + grid;
+    const bool more = next_slot < planes;
+    const int32_t next = more ? plane_of(next_slot) : 0;
     if (more) issue(st, kn, next);  // in flight while this plane is reduced
     for (int32_t qb = 0; qb < q_blocks; ++qb) query_block(kc, out_plane, qb);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
+    slot = next_slot;
     plane = next;
     return more;
   };
@@ -506,6 +522,7 @@ hipError_t launch_plane_k(Problem& p, hipStream_t s) {
   int64_t waves = static_cast<int64_t>(plane_resident_waves<T, OutT, kD, kKeys>()) *
                   (p.compute_units > 0 ? p.compute_units : 1);
   if (waves > planes) waves = planes;
+  if (waves >= 8) waves -= waves % 8;  // whole XCD rounds (see the kernel)
   void* args[] = {&p};
   return hipLaunchKernel(reinterpret_cast<const void*>(&rbf_plane_kernel<T, OutT, kD, kKeys>),
                          dim3(static_cast<unsigned>(waves)), dim3(64), args, 0, s);
