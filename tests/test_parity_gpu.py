@@ -169,6 +169,30 @@ def test_full_serving_size_properties():
     assert torch.equal(torch.ops.vectra.rbf_attention(q, k, v, scale, bias), base.to(torch.bfloat16))
 
 
+def test_full_long_key_size_properties():
+    """Config 4 at its full size (16 x 16 planes of 4096 x 4096, D = 64),
+    through properties the operator must have whatever the size."""
+    inputs = configs.make_inputs(configs.LONG_KEY, seed=4).to('cuda')
+    q, k, v, scale, bias = inputs.args()
+    assert bias is None
+    base = capi.forward(q, k, v, scale, None, out_dtype=torch.float32)
+    # Scaling V by a power of two scales every output exactly.
+    doubled = capi.forward(q, k, v * 2, scale, None, out_dtype=torch.float32)
+    assert torch.equal(doubled, base * 2)
+    # Planes and query rows are independent: a sub-batch of planes and a
+    # permutation of the query rows reproduce their outputs.
+    part = capi.forward(q[3:5, 7:9], k[3:5, 7:9], v[3:5, 7:9], scale[:, 7:9], None, out_dtype=torch.float32)
+    torch.testing.assert_close(part, base[3:5, 7:9], rtol=1e-6, atol=1e-7)
+    perm = torch.randperm(q.shape[2], generator=torch.Generator().manual_seed(1)).cuda()
+    permuted = capi.forward(q[:, :, perm], k, v, scale, None, out_dtype=torch.float32)
+    torch.testing.assert_close(permuted, base[:, :, perm], rtol=1e-6, atol=1e-7)
+    # Outputs are convex combinations of each plane's values.
+    vf = v.float()
+    lo, hi = vf.amin(2, keepdim=True), vf.amax(2, keepdim=True)
+    assert bool(((base >= lo - 1e-5) & (base <= hi + 1e-5)).all())
+    assert bool(torch.isfinite(base).all())
+
+
 def test_variants_agree_at_full_self_attention_size():
     inputs = configs.make_inputs(configs.SELF_ATTENTION, seed=3).to('cuda')
     results = {}
