@@ -472,3 +472,57 @@ def test_graph_replays_match_eager():
         assert torch.equal(static_out, eager), f'replay {i}'
         torch.ops.vectra.rbf_attention(*inputs.args())  # eager work between replays
         torch.cuda.synchronize()
+
+
+# --- A seeded sweep over the operator's input space. -------------------------
+
+def _sweep_cases(count=48):
+    """(seed, n_q, n_k, dim, value_dim, dtype, bias kind, layout) drawn from a
+    fixed seed, so the sweep is the same on every run."""
+    rng = np.random.default_rng(20261202)
+    n_qs = [1, 2, 5, 15, 16, 17, 33, 64, 65, 80, 81, 130]
+    n_ks = [1, 7, 16, 31, 64, 65, 80, 81, 128, 129, 200, 257]
+    dims = [8, 16, 32, 48, 64, 128]
+    dtypes = [torch.bfloat16, torch.float16, torch.float32]
+    cases = []
+    for i in range(count):
+        dim = int(rng.choice(dims))
+        value_dim = dim if rng.random() < 0.75 else int(rng.choice(dims))
+        cases.append((i, int(rng.choice(n_qs)), int(rng.choice(n_ks)), dim, value_dim,
+                      dtypes[int(rng.integers(3))], ['none', 'ragged', 'per_head'][int(rng.integers(3))],
+                      ['contiguous', 'transposed'][int(rng.integers(2))]))
+    return cases
+
+
+@pytest.mark.parametrize('case', _sweep_cases(), ids=lambda c: '-'.join(str(x).replace('torch.', '') for x in c))
+def test_seeded_sweep(case):
+    """Random shapes, dtypes, masks and layouts through every variant that
+    accepts them, against the float64 oracle."""
+    seed, n_q, n_k, dim, value_dim, dtype, bias_kind, layout = case
+    gen = torch.Generator().manual_seed(1000 + seed)
+    batch, heads = 2, 3
+    if layout == 'transposed':
+        # Head-transposed views of one [B, N, H * 3 * D] projection, as the model's sites.
+        def project(n, d):
+            return torch.randn(batch, n, heads * d, generator=gen).view(batch, n, heads, d).transpose(1, 2)
+        q, k, v = project(n_q, dim), project(n_k, dim), project(n_k, value_dim)
+    else:
+        q = torch.randn(batch, heads, n_q, dim, generator=gen)
+        k = torch.randn(batch, heads, n_k, dim, generator=gen)
+        v = torch.randn(batch, heads, n_k, value_dim, generator=gen)
+    scale = 0.5 / dim + 0.2 / dim * torch.rand(1, heads, 1, 1, generator=gen)
+    bias = None
+    if bias_kind == 'ragged':
+        bias = torch.zeros(batch, 1, 1, n_k)
+        bias[0, ..., max(1, n_k // 2):] = -math.inf
+    elif bias_kind == 'per_head':
+        bias = torch.randn(batch, heads, 1, n_k, generator=gen)
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    if bias is not None:
+        bias = bias.to(dtype)
+    want = oracle.expanded_fp64(q, k, v, scale, bias)
+    tol = FP32_TOL if dtype == torch.float32 else HALF_TOL
+    for variant in _variants(q, k, v, scale, bias):
+        print(f'sweep case={case} variant={variant}', flush=True)
+        got = run(q, k, v, scale, bias, variant).double().numpy()
+        np.testing.assert_allclose(got, want, equal_nan=True, err_msg=variant, **tol)
