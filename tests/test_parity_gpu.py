@@ -526,3 +526,42 @@ def test_seeded_sweep(case):
         print(f'sweep case={case} variant={variant}', flush=True)
         got = run(q, k, v, scale, bias, variant).double().numpy()
         np.testing.assert_allclose(got, want, equal_nan=True, err_msg=variant, **tol)
+
+
+def _strided_copy(small, strides, device='cuda'):
+    """`small` placed in a large zeroed buffer under the given element strides
+    (a view whose offsets need more than 32 bits)."""
+    span = 1 + sum((n - 1) * s for n, s in zip(small.shape, strides))
+    big = torch.zeros(span, dtype=small.dtype, device=device)
+    view = big.as_strided(small.shape, strides)
+    view.copy_(small.to(device))
+    return view
+
+
+def test_offsets_beyond_32_bits():
+    """Keys 1 GB apart inside a plane (per-lane 32-bit offsets would wrap: the
+    kernels that use them must decline), and planes 4 GB apart (64-bit plane
+    bases), against the float64 oracle."""
+    gen = torch.Generator().manual_seed(32)
+    q = torch.randn(2, 2, 3, 32, generator=gen).bfloat16()
+    k = torch.randn(2, 2, 3, 32, generator=gen).bfloat16()
+    v = torch.randn(2, 2, 3, 32, generator=gen).bfloat16()
+    scale = torch.tensor(0.05)
+    want = oracle.expanded_fp64(q, k, v, scale)
+    # Keys 2^29 elements (1 GB of bf16) apart within each plane.
+    far_keys = _strided_copy(k, (6 * 32, 3 * 32, 1 << 29, 1))
+    variants = _variants(q, far_keys, v, scale, None)
+    assert 'stream' not in variants, variants
+    for variant in variants:
+        got = run(q, far_keys, v, scale, None, variant).double().numpy()
+        np.testing.assert_allclose(got, want, err_msg=f'far keys {variant}', **HALF_TOL)
+    del far_keys
+    # Batch entries 2^31 elements (4 GB) apart; each plane itself is compact.
+    far_planes = _strided_copy(v, (1 << 31, 3 * 32, 32, 1))
+    variants = _variants(q, k, far_planes, scale, None)
+    assert 'stream' in variants, variants
+    for variant in variants:
+        got = run(q, k, far_planes, scale, None, variant).double().numpy()
+        np.testing.assert_allclose(got, want, err_msg=f'far planes {variant}', **HALF_TOL)
+    del far_planes
+    torch.cuda.empty_cache()
