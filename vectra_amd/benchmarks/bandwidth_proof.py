@@ -1,0 +1,187 @@
+"""HBM bytes per query and achieved HBM bandwidth, eager versus fused, from
+rocprofv3 counters.
+
+  python -m vectra_amd.benchmarks.bandwidth_proof [--batches 64 1024] [--config serving] \\
+      [--out bandwidth.json] [--work gpurun_out/bandwidth]
+
+Restates the reference's benchmark/bandwidth/run_bandwidth_proof.py:16-120
+with rocprofv3 in place of Nsight Compute.  For each batch and for both the
+eager chain and the fused operator it profiles the attention region of
+`vectra_amd.benchmarks.eager_gpu` three times: `--kernel-trace --stats` for
+the kernels' time, then `--pmc FETCH_SIZE` and `--pmc WRITE_SIZE` for HBM
+bytes (each counter scaled by what it reads for a device copy of known
+size, `vectra_amd.benchmarks.copy_calibration`).  Per call of the region:
+
+  dram_bytes            read + write bytes
+  dram_bytes_per_query  dram_bytes / batch
+  kernel_ns             time of the region's kernels
+  dram_throughput_pct   dram_bytes / kernel_ns against the 8 TB/s peak
+
+The default workload is the serving shape (B=1024, H=8, Lq=1, Lk=64, D=32,
+bf16); `--config bandwidth` is the reference's own (H=4, Lq=Lk=65, fp16).
+Each run makes 5 warm-up calls (one per rotating input set, 5 x the
+working set: above the 256 MB Infinity Cache at B=1024) and `--reps` more;
+counters are divided by that number of calls.  It then checks the gates the
+reference reads from its serving SLO:
+
+* fused / eager DRAM bytes <= 0.60 at every batch;
+* fused DRAM throughput >= 65 % of peak at the batch whose working set
+  exceeds the caches (1024), where it measures streaming, not launch latency.
+
+The analytic budgets of `vectra_amd.benchmarks.roofline` are reported
+beside the counters.  Exits 1 when a gate fails.
+"""
+
+import argparse
+import csv
+import dataclasses
+import json
+import os
+import subprocess
+import sys
+
+from vectra_amd.benchmarks import configs
+from vectra_amd.benchmarks import roofline
+from vectra_amd.benchmarks import rocprof_summary
+
+# The GPU gates of the reference's serving SLO (serving/configs/slo.yaml:21-30).
+SLO = {
+    'gpu': {
+        'dram_bytes_ratio_max': 0.60,
+        'throughput_ratio_min': 3.0,
+        'dram_throughput_pct_min': 65,
+        'numerics_rtol': 1.0e-3,
+    },
+}
+
+# The batch at which bandwidth utilisation is judged (working set > caches).
+UTILIZATION_BATCH = 1024
+
+# rocprofv3 names the runtime's copy kernels with this prefix; they move the
+# host-built inputs, not the region's data.
+RUNTIME_BLIT = rocprof_summary.RUNTIME_BLIT
+
+
+def evaluate(measured: dict, slo: dict = SLO) -> list[str]:
+    """Failures of a {batch: {impl: counters}} measurement against the SLO
+    (run_bandwidth_proof.py:66-83)."""
+    max_ratio = slo['gpu']['dram_bytes_ratio_max']
+    min_pct = slo['gpu']['dram_throughput_pct_min']
+    failures = []
+    for batch, runs in measured.items():
+        ratio = runs['fused']['dram_bytes'] / runs['eager']['dram_bytes']
+        if ratio > max_ratio:
+            failures.append(f'batch {batch}: fused/eager bytes {ratio:.3f} > {max_ratio}')
+    utilization = measured.get(UTILIZATION_BATCH)
+    if utilization is None:
+        failures.append(f'batch {UTILIZATION_BATCH} was not profiled')
+    elif utilization['fused']['dram_throughput_pct'] < min_pct:
+        achieved = utilization['fused']['dram_throughput_pct']
+        failures.append(f'fused DRAM throughput {achieved:.1f}% < {min_pct}%')
+    return failures
+
+
+def region_counter(path: str) -> float:
+    """A counter summed over every dispatch of a run (runtime copy blits excluded)."""
+    total = 0.0
+    with open(path, encoding='utf-8') as f:
+        for r in csv.DictReader(f):
+            if RUNTIME_BLIT not in r['Kernel_Name']:
+                total += float(r['Counter_Value'])
+    return total
+
+
+def region_kernel_ns(path: str) -> float:
+    """Total kernel time of a `--kernel-trace --stats` run (copy blits excluded)."""
+    total = 0.0
+    with open(path, encoding='utf-8') as f:
+        for r in csv.DictReader(f):
+            if RUNTIME_BLIT not in r['Name']:
+                total += float(r['TotalDurationNs'])
+    return total
+
+
+def region_counters(stats_csv: str, fetch_csv: str, write_csv: str, calls: int, batch: int,
+                    scales: dict) -> dict:
+    """Per-call bytes, time and throughput of a region from its three runs."""
+    read = region_counter(fetch_csv) * 1024.0 * scales['fetch_scale'] / calls
+    write = region_counter(write_csv) * 1024.0 * scales['write_scale'] / calls
+    kernel_ns = region_kernel_ns(stats_csv) / calls
+    dram_bytes = read + write
+    return {
+        'dram_bytes': dram_bytes,
+        'dram_read_bytes': read,
+        'dram_write_bytes': write,
+        'dram_bytes_per_query': dram_bytes / batch,
+        'kernel_ns': kernel_ns,
+        'dram_throughput_pct': 100.0 * dram_bytes / (kernel_ns * 1e-9) / roofline.MI355X.hbm_bytes_per_s,
+    }
+
+
+def _rocprof(args: list[str], out_dir: str, name: str, program: list[str], timeout: int) -> str:
+    """Runs `program` under rocprofv3 as a child process; returns its output directory."""
+    target = os.path.join(out_dir, name)
+    cmd = ['timeout', '-s', 'KILL', str(timeout), 'rocprofv3', *args, '--output-format', 'csv',
+           '-d', target, '-o', name, '--', *program]
+    print('+', ' '.join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    return target
+
+
+def copy_scales(work: str) -> dict:
+    """FETCH_SIZE / WRITE_SIZE bytes per counter byte, from a 512 MiB device copy."""
+    program = [sys.executable, '-m', 'vectra_amd.benchmarks.copy_calibration']
+    fetch = _rocprof(['--pmc', 'FETCH_SIZE'], work, 'copy_fetch', program, 90)
+    write = _rocprof(['--pmc', 'WRITE_SIZE'], work, 'copy_write', program, 90)
+    copy_bytes = 512 << 20
+    cf = max(rocprof_summary.counter_per_dispatch(os.path.join(fetch, 'copy_fetch_counter_collection.csv'),
+                                                  'copyBuffer'))
+    cw = max(rocprof_summary.counter_per_dispatch(os.path.join(write, 'copy_write_counter_collection.csv'),
+                                                  'copyBuffer'))
+    return {'fetch_scale': copy_bytes / (cf * 1024.0), 'write_scale': copy_bytes / (cw * 1024.0)}
+
+
+def measure(config_name: str, batch: int, impl: str, work: str, scales: dict, reps: int) -> dict:
+    program = [sys.executable, '-m', 'vectra_amd.benchmarks.eager_gpu', '--impl', impl,
+               '--config', config_name, '--batch', str(batch), '--reps', str(reps)]
+    name = f'{impl}_{batch}'
+    stats = _rocprof(['--kernel-trace', '--stats'], work, f'{name}_trace', program, 180)
+    fetch = _rocprof(['--pmc', 'FETCH_SIZE'], work, f'{name}_fetch', program, 120)
+    write = _rocprof(['--pmc', 'WRITE_SIZE'], work, f'{name}_write', program, 120)
+    calls = 5 + reps  # eager_gpu: one warm-up call per input set (5), then --reps
+    return region_counters(os.path.join(stats, f'{name}_trace_kernel_stats.csv'),
+                           os.path.join(fetch, f'{name}_fetch_counter_collection.csv'),
+                           os.path.join(write, f'{name}_write_counter_collection.csv'),
+                           calls, batch, scales)
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(description=__doc__.split('\n\n')[0])
+    p.add_argument('--config', default='serving', choices=sorted(configs.CONFIGS))
+    p.add_argument('--batches', type=int, nargs='+', default=[64, UTILIZATION_BATCH])
+    p.add_argument('--reps', type=int, default=20)
+    p.add_argument('--work', default='gpurun_out/bandwidth', help='rocprofv3 output directory')
+    p.add_argument('--out', default=None)
+    args = p.parse_args(argv)
+    os.makedirs(args.work, exist_ok=True)
+    work = os.path.abspath(args.work)
+    config = configs.CONFIGS[args.config]
+    scales = copy_scales(work)
+    measured, budgets = {}, {}
+    for batch in args.batches:
+        measured[batch] = {impl: measure(args.config, batch, impl, work, scales, args.reps)
+                           for impl in ('eager', 'fused')}
+        budgets[batch] = roofline.analyze(dataclasses.replace(config, batch=batch).shape())
+    failures = evaluate(measured)
+    report = {'config': args.config, 'copy_scales': scales, 'measured': measured,
+              'analytic_budgets': budgets, 'failures': failures, 'passed': not failures}
+    text = json.dumps(report, indent=2)
+    if args.out:
+        with open(args.out, 'w', encoding='utf-8') as f:
+            f.write(text + '\n')
+    print(json.dumps({'failures': failures, 'passed': not failures}), flush=True)
+    return 0 if not failures else 1
+
+
+if __name__ == '__main__':
+    sys.exit(main())

@@ -60,8 +60,11 @@ CPU_EAGER = Config('cpu_eager', 64, 4, 1, 32, 16, torch.float32, 0.5 / 16, (4, 3
 SERVING = Config('serving', 1024, 8, 1, 64, 32, torch.bfloat16, (0.01, 0.1), (8, 64))
 SELF_ATTENTION = Config('self_attention', 1024, 8, 65, 65, 32, torch.bfloat16, 1.0 / 32, (16, 65))
 LONG_KEY = Config('long_key', 16, 16, 4096, 4096, 64, torch.bfloat16, (0.005, 0.05), None, qk_std=0.5)
+# The reference's bandwidth-proof workload (kernels/benchmarks/bandwidth.py:44-57,
+# throughput.py:97-111): fp16, gamma = 1/(2D) in every head, the last 8 keys padded.
+BANDWIDTH = Config('bandwidth', 1024, 4, 65, 65, 32, torch.float16, (1.0 / 64, 1.0 / 64), (57, 57))
 
-CONFIGS = {c.name: c for c in (CPU_EAGER, SERVING, SELF_ATTENTION, LONG_KEY)}
+CONFIGS = {c.name: c for c in (CPU_EAGER, SERVING, SELF_ATTENTION, LONG_KEY, BANDWIDTH)}
 
 
 @dataclasses.dataclass

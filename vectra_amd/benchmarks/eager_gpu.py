@@ -1,6 +1,6 @@
 """The eager operator chain on the GPU, beside the fused operator.
 
-  python -m vectra_amd.benchmarks.eager_gpu --impl eager|fused [--config serving] [--reps 20]
+  python -m vectra_amd.benchmarks.eager_gpu --impl eager|fused [--config serving] [--batch B] [--reps 20]
 
 `eager_rbf_attention` restates the reference's eager chain
 (kernels/vectra_kernels/reference.py:46-58): the [B, H, Lq, Lk, D]
@@ -54,10 +54,11 @@ def main():
     p.add_argument('--config', default='serving', choices=sorted(configs.CONFIGS))
     p.add_argument('--sets', type=int, default=5)
     p.add_argument('--reps', type=int, default=20)
+    p.add_argument('--batch', type=int, default=None, help='first B batch entries of the config (default: all)')
     args = p.parse_args()
     config = configs.CONFIGS[args.config]
     fn = IMPLS[args.impl]
-    sets = [configs.make_inputs(config, seed=s).to('cuda') for s in range(args.sets)]
+    sets = [configs.make_inputs(config, seed=s, batch=args.batch).to('cuda') for s in range(args.sets)]
     calls = 0
     for s in sets:
         fn(*s.args())
@@ -76,6 +77,7 @@ def main():
     print(json.dumps({
         'impl': args.impl,
         'config': config.name,
+        'batch': args.batch or config.batch,
         'calls': calls,
         'median_ms': statistics.median(times),
         'dtype': str(config.dtype).replace('torch.', ''),
