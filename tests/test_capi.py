@@ -101,6 +101,22 @@ def test_variant_selection(kwargs, variant):
     assert capi.VARIANT_NAMES[capi.select_variant(_fake_args(**kwargs))] == variant
 
 
+def test_plane_kernel_needs_disjoint_rows_within_32_bit_offsets():
+    """The plane kernel reads K and V through buffer extents that end at the
+    last row, so rows past Nk read as zeros only when rows do not overlap; and
+    its offsets span up to 144 rows."""
+    assert capi.VARIANT_NAMES[capi.select_variant(_fake_args(n_q=65, n_k=65))] == 'plane'
+    h, n, d = 8, 65, 32
+    for name, row_stride in (('k_stride', 0), ('v_stride', 0), ('k_stride', 16), ('v_stride', 24)):
+        a = _fake_args(n_q=n, n_k=n)
+        setattr(a, name, (ctypes.c_int64 * 4)(h * n * 64, n * 64, row_stride, 1))
+        assert capi.VARIANT_NAMES[capi.select_variant(a)] != 'plane', (name, row_stride)
+    a = _fake_args(n_q=n, n_k=n)
+    far = 1 << 24  # 144 rows of 32 MiB overflow 32-bit offsets
+    a.q_stride = (ctypes.c_int64 * 4)(h * n * far, n * far, far, 1)
+    assert capi.VARIANT_NAMES[capi.select_variant(a)] != 'plane'
+
+
 def test_forcing_a_variant_that_cannot_run_is_an_error():
     a = _fake_args(d=24, dv=24, variant='stream')
     assert capi.select_variant(a) == -capi.ERR_BAD_VARIANT

@@ -24,7 +24,7 @@ hipError_t launch_generic(Problem& p, int in_dtype, int out_dtype, hipStream_t s
 bool mfma_supports(const Problem& p, int in_dtype, int out_dtype);
 hipError_t launch_mfma(Problem& p, int in_dtype, int out_dtype, hipStream_t s);
 
-// Plane kernel (one wave per (b, h) plane): bf16/fp16 inputs, output in the
+// Plane kernel (one workgroup per (b, h) plane): bf16/fp16 inputs, output in the
 // input dtype or fp32, D == Dv in {16, 32}, Nq and Nk both <= 80 (<= 128 for
 // 16-dim heads), unit d stride, 16-byte-aligned rows.
 bool plane_supports(const Problem& p, int in_dtype, int out_dtype);

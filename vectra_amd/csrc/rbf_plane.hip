@@ -30,6 +30,13 @@ bool plane_supports(const Problem& p, int in_dtype, int out_dtype) {
       ((p.Nk - 1) * p.sv[2] + p.Dv) * 2 > kMax32)
     return false;
   if (p.bias != nullptr && (p.Nk - 1) * p.sbn * (p.bias_dtype == VECTRA_F32 ? 4 : 2) + 4 > kMax32) return false;
+  // The kernel reads through buffer resources that end at a plane's last
+  // row, so rows past Nk read as zeros only if K and V rows do not overlap;
+  // the offsets it forms span up to 144 rows (a tile plus a query block).
+  if (p.sk[2] < p.D || p.sv[2] < p.Dv) return false;
+  constexpr int64_t kRows = 144;
+  if (kRows * p.sq[2] * 2 > kMax32 || kRows * p.sk[2] * 2 > kMax32 || kRows * p.sv[2] * 2 > kMax32) return false;
+  if (p.bias != nullptr && kRows * p.sbn * (p.bias_dtype == VECTRA_F32 ? 4 : 2) > kMax32) return false;
   // Output offsets inside a plane are 32-bit element counts.
   if (p.so[2] < 0 || p.so[3] < 0 || (p.Nq - 1) * p.so[2] + (p.Dv - 1) * p.so[3] > 0x7fffffffLL) return false;
   // Plane indices (and plane + grid size) are 32-bit.

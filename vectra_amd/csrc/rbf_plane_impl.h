@@ -1,10 +1,11 @@
-// Single-tile RBF attention on gfx950 matrix cores, one wave per (b, h)
-// plane: the kernel template, instantiated per dtype pair in
-// rbf_plane_<in>_<out>.hip.
+// Single-tile RBF attention on gfx950 matrix cores, one workgroup per (b, h)
+// plane and one wave per two 16-query blocks: the kernel template,
+// instantiated per dtype pair in rbf_plane_<in>_<out>.hip.
 //
 // For planes whose query and key axes both fit one tile (self-attention over
-// a comparable set: Lq = Lk = 65, head dims 16 and 32) the whole plane is
-// one work item of one wave, so no wave ever waits for another:
+// a comparable set: Lq = Lk = 65, head dims 16 and 32) the workgroup stages
+// the plane's K and V in LDS once, and each of its waves then computes two
+// blocks of 16 queries against every key:
 //
 //   S^T = K . Q^T     (16 keys x 16 queries per instruction)
 //   O^T = V^T . P^T   (16 value dims x 16 queries)
@@ -14,24 +15,25 @@
 // 16t + 4g + r; those of key blocks 2p and 2p + 1 are the B operand of one
 // 16x16x32 step of the second product over keys read in the order
 // {32p + 4g .. +3, 32p + 16 + 4g .. +3}, and an odd last block takes a
-// 16x16x16 step.  K stays in the registers it is loaded into as the A operand
-// of the first product (row l % 16 of each key block, head dims 8g .. 8g+7,
-// or 4g .. 4g+3 for 16-dim heads); V is written transposed into LDS.
+// 16x16x16 step.  K rows sit in LDS as loaded (the A operand of the first
+// product is row l % 16 of a key block, head dims 8g .. 8g+7, or 4g .. 4g+3
+// for 16-dim heads; read where it is used); V is written transposed; q goes
+// from HBM straight into the B operand.
 //
 // Per-score arithmetic is one FMA, one exp2 and the 16-bit split of the
 // weight:
-//  * gamma |k|^2 / 2, the key bias and the plane's largest bias M are folded
-//    once per plane into one value per key,
-//      c_j = log2(e) (bias_j - gamma |k_j|^2) - M,
+//  * gamma |k|^2 / 2 and the key bias are folded once per plane into one
+//    value per key,
+//      c_j = log2(e) (bias_j - gamma |k_j|^2),
 //    and the per-query constant -gamma |q|^2 is left out (a softmax row does
 //    not see a shift), so the exp2 argument is one FMA of the product,
-//      x = 2 gamma log2(e) q.k + c_j = log2(e) (-gamma (d - |q|^2) + bias_j) - M;
+//      x = 2 gamma log2(e) q.k + c_j = log2(e) (-gamma (d - |q|^2) + bias_j);
 //  * the softmax sum comes from the second product itself: a row of ones in
 //    the A operand sums the same hi + lo weights the values are weighted by,
 //    so the denominator needs no VALU add and no cross-lane reduction;
 //  * no running maximum is kept: if a query's weight sum leaves the range in
 //    which the 16-bit split is accurate and the value products cannot
-//    overflow (gamma < 0, a query far from every key, extreme biases), its
+//    overflow (gamma < 0, a query far from every key, biases far from 0), its
 //    block is computed once more with each query's exact maximum subtracted.
 // The distance is not clamped at zero: where rounding makes the expansion
 // negative (a query on top of a key), -d and the reference's max(d, 0) = 0
@@ -39,28 +41,37 @@
 //
 // Weights are fed to the second product as hi + lo 16-bit pairs (~2^-17 of
 // the weight), as in rbf_mfma_kernel.  Keys past Nk have c_j = -inf, and
-// their K and V rows are zeroed, so they contribute nothing.  A fully masked
+// their K and V rows read as zeros, so they contribute nothing.  A fully masked
 // row ends as 0 * (1 / 0) = NaN, as eager softmax gives.
 //
-// Scheduling: the grid is persistent (as many one-wave workgroups as fit at
-// once); a wave takes slots blockIdx.x, blockIdx.x + gridDim.x, ..., each
-// slot mapped to a plane so that an XCD works on contiguous planes.  Right
-// after a plane's operands are in place (K in registers; V^T, the folded
-// biases and q in LDS) every load of the wave's next plane is issued into
-// registers, so its HBM latency overlaps the whole of this plane's products.
-// q travels with the prefetch (and waits in LDS) because vector loads return
-// in issue order: a q load issued during the plane would wait for the whole
-// prefetch.
-
+// Scheduling: one workgroup per plane, a wave per two query blocks (three
+// waves for 65 queries).  The waves share the staging of K and V and then
+// run their blocks independently, the two blocks of a wave interleaved; the
+// hardware balances planes over the compute units as workgroups finish, and
+// the load latency of one workgroup is covered by the products of the others
+// resident on the same compute unit.  Workgroup w is mapped to a plane so
+// that an XCD works on contiguous planes.
 #pragma once
 
-#include <atomic>
+#include <type_traits>
 
 #include "rbf_common.h"
 #include "rbf_kernels.h"
 #include "rbf_mfma_ops.h"
 
 namespace vectra {
+
+// A buffer resource over `bytes` bytes from `base`: loads past the end read
+// as zeros.  Word 3 is the gfx9 data-format field of a raw buffer.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+// Cache policy of the streaming loads: non-temporal.
+constexpr int kNt = 2;
+__device__ __forceinline__ uint4 load16_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNt);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 template <int kBytes>
 struct PlaneFrag;
@@ -69,6 +80,9 @@ struct PlaneFrag<16> {
   typedef uint4 type;
   static __device__ __forceinline__ uint4 zero() { return make_uint4(0, 0, 0, 0); }
   static __device__ __forceinline__ uint4 load_stream(const void* p) { return load16_stream(p); }
+  static __device__ __forceinline__ uint4 load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return load16_buf(r, off);
+  }
 };
 template <>
 struct PlaneFrag<8> {
@@ -78,6 +92,10 @@ struct PlaneFrag<8> {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     const u32x2 r = __builtin_nontemporal_load(static_cast<const u32x2*>(p));
     return make_uint2(r.x, r.y);
+  }
+  static __device__ __forceinline__ uint2 load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kNt);
+    return make_uint2(v[0], v[1]);
   }
 };
 
@@ -115,22 +133,22 @@ __device__ __forceinline__ f32x4 plane_qk(uint2 k, uint2 q, f32x4 c) {
   using Pv = typename MfmaOps<T>::Pv;
   return MfmaOps<T>::pv(__builtin_bit_cast(Pv, k), __builtin_bit_cast(Pv, q), c);
 }
-
 template <typename T, int kD, int kKeys>
 struct PlaneGeo {
   static_assert(sizeof(T) == 2, "16-bit inputs");
   static_assert((kD == 16 || kD == 32) && kKeys % 16 == 0 && kKeys >= 32 && kKeys <= 128, "tile shape");
-  static constexpr int kNB = kKeys / 16;              // 16-key blocks (and 16-query blocks)
+  static constexpr int kNB = kKeys / 16;              // 16-key blocks (and at most as many query blocks)
   static constexpr int kFragBytes = kD == 32 ? 16 : 8;  // a lane's share of a K or q row
   using Frag = typename PlaneFrag<kFragBytes>::type;
-  // V^T rows: a multiple of 8 elements, an odd number of 16-byte units, so
-  // the 16 rows of one operand read start in distinct bank groups.
+  static constexpr int kChunks = kD / 8;  // 16-byte chunks per K or V row
+  // K rows in LDS: an odd number of 16-byte units, so the 16 rows of one
+  // operand read start in distinct bank groups.
+  static constexpr int kKStride = kD * 2 + 16;
+  static constexpr int kKChunks = kKeys * kChunks;
+  // V^T rows: a multiple of 8 elements, an odd number of 16-byte units.
   static constexpr int kVStride = kKeys + 8;
   static constexpr int kPairKeys = 32 * (kNB / 2);  // keys read by 16x16x32 steps
-  static constexpr int kVChunks = kD / 8;           // 16-byte chunks per V row
-  static constexpr int kVPairSlots = kKeys / 2 * kVChunks;
-  static constexpr int kVSlots = (kVPairSlots + kWave - 1) / kWave;
-  static constexpr int kBiasSlots = (kNB + 3) / 4;
+  static constexpr int kVPairSlots = kKeys / 2 * kChunks;
   static constexpr int kDTiles = kD / 16;
   // Position of key j in a V^T row.  Below kPairKeys each 32-key group is
   // stored as the 8-key runs {4g .. 4g+3, 16+4g .. 16+4g+3}, g = 0..3, so the
@@ -141,28 +159,22 @@ struct PlaneGeo {
   }
 };
 
-// Registers holding the loads of one plane other than K.
-template <typename T, int kD, int kKeys>
-struct PlaneStage {
-  using G = PlaneGeo<T, kD, kKeys>;
-  typename G::Frag q[G::kNB];
-  uint4 v[G::kVSlots][2];
-  uint32_t bias[G::kBiasSlots];
-  uint32_t bias_misalign;
-  RawScalar scale;
-};
+// Query blocks per wave: two, computed interleaved (their products share the
+// V^T operand reads, and each one's latencies are covered by the other's
+// instructions).
+constexpr int kPlaneBlocksPerWave = 2;
 
 template <typename T, typename OutT, int kD, int kKeys>
-__global__ __launch_bounds__(64) void rbf_plane_kernel(Problem p) {
+__global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane_kernel(Problem p) {
   using G = PlaneGeo<T, kD, kKeys>;
   using Ops = MfmaOps<T>;
   using Frag = typename G::Frag;
   using FragOps = PlaneFrag<G::kFragBytes>;
-  using Stage = PlaneStage<T, kD, kKeys>;
   using Qk = typename Ops::Qk;
   using Pv = typename Ops::Pv;
   constexpr int kNB = G::kNB;
-  constexpr int kVChunks = G::kVChunks;
+  constexpr int kPer = kPlaneBlocksPerWave;
+  constexpr int kChunks = G::kChunks;
   constexpr int kFragBytes = G::kFragBytes;
   constexpr uint32_t kOutSize = sizeof(OutT);
   // Range of a query's weight sum that needs no shift.  bf16: weights of at
@@ -174,31 +186,35 @@ __global__ __launch_bounds__(64) void rbf_plane_kernel(Problem p) {
   constexpr bool kBf16 = __is_same(T, __bf16);
   constexpr float kSumHi = kBf16 ? 0x1p32f : 0x1p15f;
   constexpr float kSumLo = kBf16 ? 0x1p-32f : 0x1p-3f;
+  // K pieces a lane loads before the first wait: the whole of K when the
+  // workgroup has at least kKeys * kD / 1024 waves (three for 65 queries
+  // over 80 keys of 32 dims); smaller workgroups loop for the rest.
+  constexpr int kKRounds = 2;
 
   __shared__ __align__(16) T vt_lds[kD * G::kVStride];
-  __shared__ __align__(16) float bias_lds[kKeys];
-  __shared__ __align__(16) Frag q_lds[kNB][kWave];
+  __shared__ __align__(16) char k_lds[kKeys * G::kKStride];
+  __shared__ __align__(16) float c_lds[kKeys];  // folded key values
 
-  const int lane = threadIdx.x;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int nthreads = static_cast<int>(blockDim.x);
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
   const int col = lane & 15;
   const int grp = lane >> 4;
 
-  const int32_t planes = static_cast<int32_t>(p.B * p.H);
-  int32_t slot = static_cast<int32_t>(blockIdx.x);
-  if (slot >= planes) return;  // one-wave workgroups: no barrier to miss
   // XCD-local plane order.  Workgroups are dispatched round-robin over the 8
-  // XCDs, so with a grid and a plane count that are multiples of 8, slot s
-  // runs on XCD s % 8; giving XCD x the contiguous planes x * planes / 8 ..
-  // puts the heads of one batch entry on one XCD at the same time.  Where
-  // q, k and v are head-transposed views of one projection (the model's
-  // sites), a cache line holds rows of several heads, and its L2 then
-  // fetches it from HBM once instead of once per XCD.  A bijection of
-  // [0, planes).
-  const int32_t grid = static_cast<int32_t>(gridDim.x);
-  const bool xcd_order = grid % 8 == 0 && planes % 8 == 0;
-  const int32_t per_xcd = planes / 8;
-  auto plane_of = [&](int32_t s) { return xcd_order ? (s & 7) * per_xcd + (s >> 3) : s; };
-  int32_t plane = plane_of(slot);
+  // XCDs, so with a plane count that is a multiple of 8, workgroup w runs on
+  // XCD w % 8; giving XCD x the contiguous planes x * planes / 8 .. puts the
+  // heads of one batch entry on one XCD at the same time.  Where q, k and v
+  // are head-transposed views of one projection (the model's sites), a cache
+  // line holds rows of several heads, and its L2 then fetches it from HBM
+  // once instead of once per XCD.  A bijection of [0, planes).
+  const int32_t planes = static_cast<int32_t>(p.B * p.H);
+  const int32_t w = static_cast<int32_t>(blockIdx.x);
+  const int32_t plane = planes % 8 == 0 ? (w & 7) * (planes / 8) + (w >> 3) : w;
+  const int32_t b = static_cast<int32_t>(fast_div(static_cast<uint32_t>(plane), p.h_mul, p.h_shift));
+  const int32_t h = plane - b * static_cast<int32_t>(p.H);
+
   const int32_t n_q = static_cast<int32_t>(p.Nq);
   const int32_t n_k = static_cast<int32_t>(p.Nk);
   const int32_t q_blocks = (n_q + 15) / 16;
@@ -212,240 +228,280 @@ __global__ __launch_bounds__(64) void rbf_plane_kernel(Problem p) {
   const bool out_vec = p.so[3] == 1 && p.so[2] % 4 == 0 && p.so[1] % 4 == 0 && p.so[0] % 4 == 0 &&
                        (reinterpret_cast<uintptr_t>(p.out) & 15u) == 0;
 
-  auto plane_bh = [&](int32_t pl, int32_t& b, int32_t& h) {
-    b = static_cast<int32_t>(fast_div(static_cast<uint32_t>(pl), p.h_mul, p.h_shift));
-    h = pl - b * static_cast<int32_t>(p.H);
+  // Loads go through buffer resources whose extent ends at the last row of
+  // the plane (rows past Nq or Nk read as zeros, a bounds check of the
+  // hardware), with one per-lane offset computed once and per-round parts in
+  // scalar registers.  Piece i of K is row i / kChunks, 16-byte chunk
+  // i % kChunks; V pair slot i is rows 2 (i / kChunks) and + 1 of the same
+  // chunk.  No row offset reaches 2^32 (the host checks (kKeys + 1) rows).
+  const char* kp = static_cast<const char*>(p.k) + (b * p.sk[0] + h * p.sk[1]) * 2;
+  const char* vp = static_cast<const char*>(p.v) + (b * p.sv[0] + h * p.sv[1]) * 2;
+  const char* qp = static_cast<const char*>(p.q) + (b * p.sq[0] + h * p.sq[1]) * 2;
+  const auto k_rsrc = plane_rsrc(kp, static_cast<uint32_t>(n_k - 1) * k_row_bytes + kD * 2);
+  const auto v_rsrc = plane_rsrc(vp, static_cast<uint32_t>(n_k - 1) * v_row_bytes + kD * 2);
+  const auto q_rsrc = plane_rsrc(qp, static_cast<uint32_t>(n_q - 1) * q_row_bytes + kD * 2);
+  const uint32_t chunk_off = static_cast<uint32_t>(lane % kChunks) * 16u;
+  const uint32_t lane_rows = static_cast<uint32_t>(lane / kChunks);  // row of a piece within a round
+  const uint32_t k_lane = lane_rows * k_row_bytes + chunk_off;
+  const uint32_t v_lane = 2u * lane_rows * v_row_bytes + chunk_off;
+  constexpr int kRowsPerWave = kWave / kChunks;  // K rows (V row pairs) a wave covers per round
+
+  // The coefficient and, per key, the folded value
+  //   c_j = log2(e) (bias_j - gamma |k_j|^2)    (-inf past Nk)
+  // computed by the lane holding the first chunk of K row j.
+  const RawScalar scale_raw = load_raw_scalar(p.scale, b * p.ssb + h * p.ssh, p.scale_dtype);
+  const char* const bp =
+      has_bias ? static_cast<const char*>(p.bias) + (b * p.sbb + h * p.sbh) * bias_esize : nullptr;
+  const uint32_t bias_key_bytes = static_cast<uint32_t>(p.sbn) * static_cast<uint32_t>(bias_esize);
+  const auto b_rsrc = plane_rsrc(bp, static_cast<uint32_t>(n_k - 1) * bias_key_bytes + bias_esize);
+  const uint32_t b_lane = lane_rows * bias_key_bytes;
+  // Raw bits of key `row0 + lane / kChunks`'s bias (an fp32 word, or a
+  // 16-bit element zero-extended).
+  auto bias_of = [&](int row0) -> uint32_t {
+    if (!has_bias) return 0u;
+    const uint32_t off = b_lane + static_cast<uint32_t>(row0) * bias_key_bytes;
+    return p.bias_dtype == VECTRA_F32 ? __builtin_amdgcn_raw_buffer_load_b32(b_rsrc, off, 0, kNt)
+                                      : __builtin_amdgcn_raw_buffer_load_b16(b_rsrc, off, 0, kNt);
   };
-
-  // Per-lane byte offsets inside a plane of the first row each load slot
-  // reads, and of the last row (every offset is clamped to it, so rows past
-  // Nq or Nk read the last row, in bounds, and no load is behind a
-  // data-dependent branch).  Slot t of K and q is rows 16t + col, slot s of
-  // V the row pair starting at 2 * (lane / chunks) + s * 128 / chunks.
-  const uint32_t frag_off = static_cast<uint32_t>(grp * kFragBytes);
-  const uint32_t k_first = static_cast<uint32_t>(col) * k_row_bytes + frag_off;
-  const uint32_t k_last = static_cast<uint32_t>(n_k - 1) * k_row_bytes + frag_off;
-  const uint32_t q_first = static_cast<uint32_t>(col) * q_row_bytes + frag_off;
-  const uint32_t q_last = static_cast<uint32_t>(n_q - 1) * q_row_bytes + frag_off;
-  const uint32_t chunk_off = static_cast<uint32_t>(lane % kVChunks) * 16u;
-  const uint32_t v_first = static_cast<uint32_t>(2 * (lane / kVChunks)) * v_row_bytes + chunk_off;
-  const uint32_t v_last = static_cast<uint32_t>(n_k - 1) * v_row_bytes + chunk_off;
-
-  // Issues every load of plane `pl`: K into `kdst` (the A operand of the
-  // first product, as loaded), the rest into `st`.  Rows past Nk are copies
-  // of row Nk - 1; their folded key value is -inf, so their weights are 0.
-  auto issue = [&](Stage& st, Frag (&kdst)[kNB], int32_t pl) {
-    int32_t b, h;
-    plane_bh(pl, b, h);
-    const char* kp = static_cast<const char*>(p.k) + (b * p.sk[0] + h * p.sk[1]) * 2;
-    const char* vp = static_cast<const char*>(p.v) + (b * p.sv[0] + h * p.sv[1]) * 2;
-    const char* qp = static_cast<const char*>(p.q) + (b * p.sq[0] + h * p.sq[1]) * 2;
-    // Opaque copies: offsets derived from them are recomputed here (one add
-    // and one min per load) instead of being hoisted into a register each.
-    uint32_t kf0 = k_first, qf0 = q_first, vf0 = v_first;
-    asm volatile("" : "+v"(kf0), "+v"(qf0), "+v"(vf0));
-#pragma unroll
-    for (int t = 0; t < kNB; ++t)
-      kdst[t] = FragOps::load_stream(kp + min(kf0 + 16u * t * k_row_bytes, k_last));
-#pragma unroll
-    for (int t = 0; t < kNB; ++t)
-      st.q[t] = FragOps::load_stream(qp + min(qf0 + 16u * t * q_row_bytes, q_last));
-#pragma unroll
-    for (int s = 0; s < G::kVSlots; ++s) {
-      if (lane + kWave * s < G::kVPairSlots) {
-        const uint32_t first = vf0 + static_cast<uint32_t>(s * 128 / kVChunks) * v_row_bytes;
-        st.v[s][0] = load16_stream(vp + min(first, v_last));
-        st.v[s][1] = load16_stream(vp + min(first + v_row_bytes, v_last));
-      }
-    }
-    if (has_bias) {
-      const char* bp = static_cast<const char*>(p.bias) + (b * p.sbb + h * p.sbh) * bias_esize;
-      st.bias_misalign = base_misalign(bp);
-#pragma unroll
-      for (int i = 0; i < G::kBiasSlots; ++i) {
-        const uint32_t key = static_cast<uint32_t>(min(16 * (grp + 4 * i) + col, n_k - 1));
-        st.bias[i] = load_raw_scalar32(bp, st.bias_misalign, key * static_cast<uint32_t>(p.sbn), p.bias_dtype).word;
-      }
-    }
-    st.scale = load_raw_scalar(p.scale, b * p.ssb + h * p.ssh, p.scale_dtype);
+  auto k_piece = [&](int row0) {
+    return load16_buf(k_rsrc, k_lane + static_cast<uint32_t>(row0) * k_row_bytes);
   };
-
-  float coef = 0.f;
-
-  // Puts a staged plane in place: V^T, the folded key values and q into LDS
-  // (K stays in the registers `kc` it was loaded into).
-  auto publish = [&](const Stage& st, const Frag (&kc)[kNB]) {
-    coef = 2.f * kLog2e * decode_raw_scalar(st.scale, p.scale_dtype);
-    float k_sq[kNB];
+  auto v_pair = [&](int row0, uint4& r0, uint4& r1) {
+    const uint32_t off = v_lane + static_cast<uint32_t>(row0) * v_row_bytes;
+    r0 = load16_buf(v_rsrc, off);
+    r1 = load16_buf(v_rsrc, off + v_row_bytes);
+  };
+  const int k_base = wave * kWave;  // first K piece (and V pair slot) of this wave
+  uint4 kr[kKRounds];
+  uint32_t bias_r[kKRounds];
 #pragma unroll
-    for (int t = 0; t < kNB; ++t)
-      k_sq[t] = allreduce_bit32(allreduce_bit16(frag_norm<T>(kc[t]), OpSum()), OpSum());
-    // Biases (log2 units) of keys 16t + col for t = grp + 4i; -inf past Nk.
-    float bl[G::kBiasSlots];
-    float top = -INFINITY;
+  for (int r = 0; r < kKRounds; ++r) {
+    kr[r] = make_uint4(0, 0, 0, 0);
+    bias_r[r] = 0;
+    const int base = k_base + r * nthreads;
+    if (base < G::kKChunks) {
+      kr[r] = k_piece(base / kChunks);
+      bias_r[r] = bias_of(base / kChunks);
+    }
+  }
+  uint4 v0a = make_uint4(0, 0, 0, 0), v0b = v0a;
+  if (k_base < G::kVPairSlots) v_pair(2 * (k_base / kChunks), v0a, v0b);
+  // This wave's query blocks: kPer * wave + j, j < blocks (1 or 2).
+  const int first_block = kPer * wave;
+  const int blocks = min(kPer, q_blocks - first_block);
+  const uint32_t q_lane = static_cast<uint32_t>(col) * q_row_bytes + static_cast<uint32_t>(grp * kFragBytes);
+  Frag qf[kPer];
 #pragma unroll
-    for (int i = 0; i < G::kBiasSlots; ++i) {
-      const int32_t key = 16 * (grp + 4 * i) + col;
-      float x = -INFINITY;
-      if (grp + 4 * i < kNB && key < n_k) {
-        x = 0.f;
+  for (int j = 0; j < kPer; ++j)
+    qf[j] = FragOps::load_buf(q_rsrc, q_lane + static_cast<uint32_t>(16 * (first_block + j)) * q_row_bytes);
+  const float coef = 2.f * kLog2e * decode_raw_scalar(scale_raw, p.scale_dtype);
+  const float half_coef = -0.5f * coef;
+
+  // K into LDS as loaded, and each row's folded value (the kChunks lanes of
+  // a row are adjacent; every lane of a wave takes part in the reduction).
+  auto put_k = [&](int base, uint4 piece, uint32_t bias_raw) {
+    const int row = base / kChunks + static_cast<int>(lane_rows);
+    const float sq = reduce_low<kChunks>(frag_norm<T>(piece), OpSum());
+    if (base + lane < G::kKChunks) {
+      *reinterpret_cast<uint4*>(k_lds + row * G::kKStride + static_cast<int>(chunk_off)) = piece;
+      if (chunk_off == 0) {
+        float x = 0.f;
         if (has_bias) {
-          const uint32_t bytes = static_cast<uint32_t>(key) * static_cast<uint32_t>(p.sbn) * bias_esize +
-                                 st.bias_misalign;
-          x = decode_raw_scalar(RawScalar{st.bias[i], (bytes & 2u) * 8u}, p.bias_dtype) * kLog2e;
+          x = p.bias_dtype == VECTRA_F32    ? __uint_as_float(bias_raw)
+              : p.bias_dtype == VECTRA_BF16 ? __uint_as_float(bias_raw << 16)
+                                            : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bias_raw)));
         }
-      }
-      bl[i] = x;
-      top = fmaxf(top, x);
-    }
-    top = reduce_wave(top, OpMax());
-    if (top == -INFINITY) top = 0.f;  // every key masked: the rows end as NaN
-#pragma unroll
-    for (int i = 0; i < G::kBiasSlots; ++i) {
-      const int t = grp + 4 * i;
-      if (t < kNB) {
-        // k_sq[4i + grp], picked by the lane group (the same three masks
-        // serve every slot).
-        float sq = k_sq[4 * i];
-        if (4 * i + 1 < kNB) sq = grp == 1 ? k_sq[4 * i + 1] : sq;
-        if (4 * i + 2 < kNB) sq = grp == 2 ? k_sq[4 * i + 2] : sq;
-        if (4 * i + 3 < kNB) sq = grp == 3 ? k_sq[4 * i + 3] : sq;
-        bias_lds[16 * t + col] = fmaf(-0.5f * coef, sq, bl[i] - top);
+        c_lds[row] = row < n_k ? fmaf(half_coef, sq, x * kLog2e) : -INFINITY;
       }
     }
-    // V^T: two keys of one value dim per 32-bit word; rows past Nk zeroed
-    // (their weight is 0, and 0 * a non-finite copy would not be).
-#pragma unroll
-    for (int s = 0; s < G::kVSlots; ++s) {
-      const int slot = lane + kWave * s;
-      if (slot < G::kVPairSlots) {
-        const int row = 2 * (slot / kVChunks);
-        const int d0 = (slot % kVChunks) * 8;
-        const uint4 r0 = row < n_k ? st.v[s][0] : make_uint4(0, 0, 0, 0);
-        const uint4 r1 = row + 1 < n_k ? st.v[s][1] : make_uint4(0, 0, 0, 0);
-        const uint32_t w0[4] = {r0.x, r0.y, r0.z, r0.w};
-        const uint32_t w1[4] = {r1.x, r1.y, r1.z, r1.w};
-        T* dst = vt_lds + d0 * G::kVStride + G::vt_pos(row);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // Elements 2e and 2e + 1 of the chunk, for keys row and row + 1.
-          *reinterpret_cast<uint32_t*>(dst + 2 * e * G::kVStride) = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u);
-          *reinterpret_cast<uint32_t*>(dst + (2 * e + 1) * G::kVStride) =
-              __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u);
-        }
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < kNB; ++t) q_lds[t][lane] = st.q[t];
   };
+  // V^T: two keys of one value dim per 32-bit word (rows past Nk read as
+  // zeros: their weight is 0, and 0 * a non-finite value would not be).
+  auto put_v = [&](int i, uint4 r0, uint4 r1) {
+    const int row = 2 * (i / kChunks);
+    const int d0 = (i % kChunks) * 8;
+    const uint32_t w0[4] = {r0.x, r0.y, r0.z, r0.w};
+    const uint32_t w1[4] = {r1.x, r1.y, r1.z, r1.w};
+    T* dst = vt_lds + d0 * G::kVStride + G::vt_pos(row);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // Elements 2e and 2e + 1 of the chunk, for keys row and row + 1.
+      *reinterpret_cast<uint32_t*>(dst + 2 * e * G::kVStride) = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u);
+      *reinterpret_cast<uint32_t*>(dst + (2 * e + 1) * G::kVStride) = __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u);
+    }
+  };
+#pragma unroll
+  for (int r = 0; r < kKRounds; ++r) {
+    const int base = k_base + r * nthreads;
+    if (base < G::kKChunks) put_k(base, kr[r], bias_r[r]);
+  }
+  if (tid < G::kVPairSlots) put_v(tid, v0a, v0b);
+  // Workgroups with fewer waves (fewer query blocks) stage the rest in
+  // further rounds.
+  for (int base = k_base + kKRounds * nthreads; base < G::kKChunks; base += nthreads)
+    put_k(base, k_piece(base / kChunks), bias_of(base / kChunks));
+  for (int base = k_base + nthreads; base < G::kVPairSlots; base += nthreads) {
+    uint4 r0, r1;
+    v_pair(2 * (base / kChunks), r0, r1);
+    if (base + lane < G::kVPairSlots) put_v(base + lane, r0, r1);
+  }
+  static_assert(kRowsPerWave * kChunks == kWave, "pieces of whole rows per wave");
+
+  __syncthreads();  // K, the folded key values and V^T in place
+
+  // Key block t's operand of the first product (read from LDS where it is
+  // used rather than held across the pass, which would cost a wave slot).
+  const char* const k_op = k_lds + col * G::kKStride + grp * kFragBytes;
+  auto kc = [&](int t) { return *reinterpret_cast<const Frag*>(k_op + 16 * t * G::kKStride); };
 
   const uint32_t one = Ops::kOnePair;
   const Qk ones8 = __builtin_bit_cast(Qk, make_uint4(one, one, one, one));
   const Pv ones4 = __builtin_bit_cast(Pv, make_uint2(one, one));
 
-  // One block of 16 query rows against every key of the plane; `out_plane`
-  // is the plane's output base.
+  // The wave's query blocks against every key of the plane.
   //
-  // The logits are taken relative to the plane's largest bias, without the
-  // per-query constant -gamma |q|^2 (softmax does not see a per-row shift):
-  //   x = 2 gamma log2(e) q.k + c_j = log2(e) (-gamma (d - |q|^2) + bias_j) - M.
+  // The logits are taken without the per-query constant -gamma |q|^2
+  // (softmax does not see a per-row shift):
+  //   x = 2 gamma log2(e) q.k + c_j = log2(e) (-gamma (d - |q|^2) + bias_j).
   // exp2(x) is used unshifted unless the weights' sum, read off the ones
   // product, leaves the range where the 16-bit split of the weights is
   // accurate and the value products cannot overflow; then the block is
   // computed once more with each query's exact maximum subtracted.
-  auto query_block = [&](const Frag (&kc)[kNB], char* out_plane, int32_t qb) {
-    // The folded key values are re-read from LDS per block rather than held
-    // in registers across blocks.
-    asm volatile("" ::: "memory");
-    const Frag qf = q_lds[qb][lane];
-    f32x4 acc[G::kDTiles];
-    f32x4 total;
-    // Weights of block t as packed 16-bit hi / lo pairs (keys 4g + 0,1 and 4g + 2,3).
-    auto weights = [&](const float (&xt)[4], uint32_t* hi, uint32_t* lo) {
-      const float w0 = __builtin_amdgcn_exp2f(xt[0]), w1 = __builtin_amdgcn_exp2f(xt[1]);
-      const float w2 = __builtin_amdgcn_exp2f(xt[2]), w3 = __builtin_amdgcn_exp2f(xt[3]);
-      Ops::split2(w0, w1, hi[0], lo[0]);
-      Ops::split2(w2, w3, hi[1], lo[1]);
-    };
-    // Logits of key block t (relative to `shift`, per query column).
-    auto logits = [&](int t, float shift, float (&xt)[4]) {
-      const f32x4 s = plane_qk<T>(kc[t], qf, f32x4{0.f, 0.f, 0.f, 0.f});
-      const float4 c = *reinterpret_cast<const float4*>(bias_lds + 16 * t + 4 * grp);
-      xt[0] = fmaf(coef, s[0], c.x - shift);
-      xt[1] = fmaf(coef, s[1], c.y - shift);
-      xt[2] = fmaf(coef, s[2], c.z - shift);
-      xt[3] = fmaf(coef, s[3], c.w - shift);
-    };
-    // One pass over the keys, block pair by block pair, so only the logits
-    // of two blocks are live at a time.
-    auto pass = [&](float shift) {
+  f32x4 acc[kPer][G::kDTiles];
+  f32x4 total[kPer];
+  // Weights of block t as packed 16-bit hi / lo pairs (keys 4g + 0,1 and 4g + 2,3).
+  auto weights = [&](const float (&xt)[4], uint32_t* hi, uint32_t* lo) {
+    const float w0 = __builtin_amdgcn_exp2f(xt[0]), w1 = __builtin_amdgcn_exp2f(xt[1]);
+    const float w2 = __builtin_amdgcn_exp2f(xt[2]), w3 = __builtin_amdgcn_exp2f(xt[3]);
+    Ops::split2(w0, w1, hi[0], lo[0]);
+    Ops::split2(w2, w3, hi[1], lo[1]);
+  };
+  // Logits of key block t for query block j (relative to `shift`, per query column).
+  auto logits = [&](int j, int t, float shift, float (&xt)[4]) {
+    const f32x4 s = plane_qk<T>(kc(t), qf[j], f32x4{0.f, 0.f, 0.f, 0.f});
+    const float4 c = *reinterpret_cast<const float4*>(c_lds + 16 * t + 4 * grp);
+    xt[0] = fmaf(coef, s[0], c.x - shift);
+    xt[1] = fmaf(coef, s[1], c.y - shift);
+    xt[2] = fmaf(coef, s[2], c.z - shift);
+    xt[3] = fmaf(coef, s[3], c.w - shift);
+  };
+  // One pass over the keys for the first `n` query blocks, block pair by
+  // block pair of keys, so only the logits of two key blocks per query
+  // block are live at a time.
+  auto pass = [&](auto n_tag, const float (&shift)[kPer]) {
+    constexpr int n = decltype(n_tag)::value;
 #pragma unroll
-      for (int u = 0; u < G::kDTiles; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      total = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < n; ++j) {
 #pragma unroll
-      for (int pp = 0; pp < kNB / 2; ++pp) {
+      for (int u = 0; u < G::kDTiles; ++u) acc[j][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      total[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int pp = 0; pp < kNB / 2; ++pp) {
+      Qk p_hi[n], p_lo[n];
+#pragma unroll
+      for (int j = 0; j < n; ++j) {
         float x0[4], x1[4];
-        logits(2 * pp, shift, x0);
-        logits(2 * pp + 1, shift, x1);
+        logits(j, 2 * pp, shift[j], x0);
+        logits(j, 2 * pp + 1, shift[j], x1);
         uint32_t hi[4], lo[4];
         weights(x0, hi, lo);
         weights(x1, hi + 2, lo + 2);
-        const Qk p_hi = __builtin_bit_cast(Qk, make_uint4(hi[0], hi[1], hi[2], hi[3]));
-        const Qk p_lo = __builtin_bit_cast(Qk, make_uint4(lo[0], lo[1], lo[2], lo[3]));
-#pragma unroll
-        for (int u = 0; u < G::kDTiles; ++u) {
-          const Qk a = *reinterpret_cast<const Qk*>(vt_lds + (16 * u + col) * G::kVStride + 32 * pp + 8 * grp);
-          acc[u] = Ops::qk(a, p_hi, acc[u]);
-          acc[u] = Ops::qk(a, p_lo, acc[u]);
-        }
-        total = Ops::qk(ones8, p_hi, total);
-        total = Ops::qk(ones8, p_lo, total);
-        __builtin_amdgcn_sched_barrier(0);
+        p_hi[j] = __builtin_bit_cast(Qk, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+        p_lo[j] = __builtin_bit_cast(Qk, make_uint4(lo[0], lo[1], lo[2], lo[3]));
       }
-      if constexpr (kNB % 2 == 1) {
-        constexpr int t = kNB - 1;
+#pragma unroll
+      for (int u = 0; u < G::kDTiles; ++u) {
+        const Qk a = *reinterpret_cast<const Qk*>(vt_lds + (16 * u + col) * G::kVStride + 32 * pp + 8 * grp);
+#pragma unroll
+        for (int j = 0; j < n; ++j) {
+          acc[j][u] = Ops::qk(a, p_hi[j], acc[j][u]);
+          acc[j][u] = Ops::qk(a, p_lo[j], acc[j][u]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < n; ++j) {
+        total[j] = Ops::qk(ones8, p_hi[j], total[j]);
+        total[j] = Ops::qk(ones8, p_lo[j], total[j]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (kNB % 2 == 1) {
+      constexpr int t = kNB - 1;
+      Pv p_hi[n], p_lo[n];
+#pragma unroll
+      for (int j = 0; j < n; ++j) {
         float x0[4];
-        logits(t, shift, x0);
+        logits(j, t, shift[j], x0);
         uint32_t hi[2], lo[2];
         weights(x0, hi, lo);
-        const Pv p_hi = __builtin_bit_cast(Pv, make_uint2(hi[0], hi[1]));
-        const Pv p_lo = __builtin_bit_cast(Pv, make_uint2(lo[0], lo[1]));
+        p_hi[j] = __builtin_bit_cast(Pv, make_uint2(hi[0], hi[1]));
+        p_lo[j] = __builtin_bit_cast(Pv, make_uint2(lo[0], lo[1]));
+      }
 #pragma unroll
-        for (int u = 0; u < G::kDTiles; ++u) {
-          const Pv a = *reinterpret_cast<const Pv*>(vt_lds + (16 * u + col) * G::kVStride + 16 * t + 4 * grp);
-          acc[u] = Ops::pv(a, p_hi, acc[u]);
-          acc[u] = Ops::pv(a, p_lo, acc[u]);
+      for (int u = 0; u < G::kDTiles; ++u) {
+        const Pv a = *reinterpret_cast<const Pv*>(vt_lds + (16 * u + col) * G::kVStride + 16 * t + 4 * grp);
+#pragma unroll
+        for (int j = 0; j < n; ++j) {
+          acc[j][u] = Ops::pv(a, p_hi[j], acc[j][u]);
+          acc[j][u] = Ops::pv(a, p_lo[j], acc[j][u]);
         }
-        total = Ops::pv(ones4, p_hi, total);
-        total = Ops::pv(ones4, p_lo, total);
       }
-    };
-    // Each query's exact maximum logit (the rare second pass).
-    auto row_max = [&]() {
-      float top = -INFINITY;
 #pragma unroll
-      for (int t = 0; t < kNB; ++t) {
-        float xt[4];
-        logits(t, 0.f, xt);
-        top = fmaxf(top, fmaxf(fmaxf(xt[0], xt[1]), fmaxf(xt[2], xt[3])));
+      for (int j = 0; j < n; ++j) {
+        total[j] = Ops::pv(ones4, p_hi[j], total[j]);
+        total[j] = Ops::pv(ones4, p_lo[j], total[j]);
       }
-      top = allreduce_bit32(allreduce_bit16(top, OpMax()), OpMax());
-      return top == -INFINITY ? 0.f : top;  // every key masked: the row ends as NaN
-    };
-    pass(0.f);
-    // Every row of the ones product holds the full sum of this query's
-    // weights.  NaN (a NaN input) fails the test and is recomputed to NaN.
-    if (__builtin_amdgcn_ballot_w64(!(total[0] >= kSumLo && total[0] <= kSumHi))) pass(row_max());
+    }
+  };
+  // Each query's exact maximum logit in block j (the rare second pass).
+  auto row_max = [&](int j) {
+    float rmax = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < kNB; ++t) {
+      float xt[4];
+      logits(j, t, 0.f, xt);
+      rmax = fmaxf(rmax, fmaxf(fmaxf(xt[0], xt[1]), fmaxf(xt[2], xt[3])));
+    }
+    rmax = allreduce_bit32(allreduce_bit16(rmax, OpMax()), OpMax());
+    return rmax == -INFINITY ? 0.f : rmax;  // every key masked: the row ends as NaN
+  };
+  // Every row of the ones product holds the full sum of a query's weights.
+  // NaN (a NaN input) fails the test and is recomputed to NaN.  A block
+  // that needs no shift is recomputed unshifted, to the same result.
+  auto run = [&](auto n_tag) {
+    constexpr int n = decltype(n_tag)::value;
+    float shift[kPer] = {};
+    pass(n_tag, shift);
+    bool again = false;
+#pragma unroll
+    for (int j = 0; j < n; ++j) {
+      if (__builtin_amdgcn_ballot_w64(!(total[j][0] >= kSumLo && total[j][0] <= kSumHi))) {
+        shift[j] = row_max(j);
+        again = true;
+      }
+    }
+    if (again) pass(n_tag, shift);
+  };
+  if (blocks == kPer) {
+    run(std::integral_constant<int, kPer>{});
+  } else {
+    run(std::integral_constant<int, 1>{});
+  }
 
-    const int32_t q_row = 16 * qb + col;
-    if (q_row < n_q) {
+  char* out_plane = static_cast<char*>(p.out) + (b * p.so[0] + h * p.so[1]) * static_cast<int64_t>(kOutSize);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int32_t out_q = 16 * (first_block + j) + col;
+    if (j < blocks && out_q < n_q) {
       // A fully masked row has sum 0 and ends as 0 * inf = NaN.
-      const float inv = __builtin_amdgcn_rcpf(total[0]);
-      const uint32_t row_off = static_cast<uint32_t>(q_row) * o_row;
+      const float inv = __builtin_amdgcn_rcpf(total[j][0]);
+      const uint32_t row_off = static_cast<uint32_t>(out_q) * o_row;
 #pragma unroll
       for (int u = 0; u < G::kDTiles; ++u) {
         const uint32_t off = (row_off + static_cast<uint32_t>(16 * u + 4 * grp) * o_dim) * kOutSize;
-        const float y0 = acc[u][0] * inv, y1 = acc[u][1] * inv, y2 = acc[u][2] * inv, y3 = acc[u][3] * inv;
+        const float y0 = acc[j][u][0] * inv, y1 = acc[j][u][1] * inv, y2 = acc[j][u][2] * inv,
+                    y3 = acc[j][u][3] * inv;
         if constexpr (kOutSize == 4) {
           if (out_vec) {
             *reinterpret_cast<float4*>(out_plane + off) = make_float4(y0, y1, y2, y3);
@@ -467,65 +523,21 @@ __global__ __launch_bounds__(64) void rbf_plane_kernel(Problem p) {
         }
       }
     }
-  };
-
-  // One plane: its K is in `kc`; the next plane's K goes to `kn`.  Returns
-  // false after the wave's last plane.
-  Stage st;
-  auto step = [&](const Frag (&kc)[kNB], Frag (&kn)[kNB]) -> bool {
-    publish(st, kc);
-    // LDS is private to the wave and its instructions run in order; the
-    // fence only keeps the compiler from moving LDS accesses across here.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    int32_t b, h;
-    plane_bh(plane, b, h);
-    char* out_plane = static_cast<char*>(p.out) + (b * p.so[0] + h * p.so[1]) * static_cast<int64_t>(kOutSize);
-    const int32_t next_slot = slot + grid;
-    const bool more = next_slot < planes;
-    const int32_t next = more ? plane_of(next_slot) : 0;
-    if (more) issue(st, kn, next);  // in flight while this plane is reduced
-    for (int32_t qb = 0; qb < q_blocks; ++qb) query_block(kc, out_plane, qb);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    slot = next_slot;
-    plane = next;
-    return more;
-  };
-
-  Frag k0[kNB], k1[kNB];
-  issue(st, k0, plane);
-  while (step(k0, k1) && step(k1, k0)) {
   }
 }
 
 // ------------------------------------------------------------------- host
 
-// One-wave workgroups of an instantiation that fit on a compute unit at once.
-template <typename T, typename OutT, int kD, int kKeys>
-int plane_resident_waves() {
-  static std::atomic<int> cached{0};
-  int n = cached.load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &n, reinterpret_cast<const void*>(&rbf_plane_kernel<T, OutT, kD, kKeys>), 64, 0) != hipSuccess ||
-        n < 1)
-      n = 1;
-    cached.store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
+// One workgroup per plane, one wave per two 16-query blocks.
 template <typename T, typename OutT, int kD, int kKeys>
 hipError_t launch_plane_k(Problem& p, hipStream_t s) {
   const int64_t planes = p.B * p.H;
-  int64_t waves = static_cast<int64_t>(plane_resident_waves<T, OutT, kD, kKeys>()) *
-                  (p.compute_units > 0 ? p.compute_units : 1);
-  if (waves > planes) waves = planes;
-  if (waves >= 8) waves -= waves % 8;  // whole XCD rounds (see the kernel)
+  const int64_t q_blocks = (p.Nq + 15) / 16;
+  const int64_t waves = (q_blocks + kPlaneBlocksPerWave - 1) / kPlaneBlocksPerWave;
+  if (planes < 1 || q_blocks < 1 || q_blocks > kKeys / 16) return hipErrorInvalidValue;
   void* args[] = {&p};
   return hipLaunchKernel(reinterpret_cast<const void*>(&rbf_plane_kernel<T, OutT, kD, kKeys>),
-                         dim3(static_cast<unsigned>(waves)), dim3(64), args, 0, s);
+                         dim3(static_cast<unsigned>(planes)), dim3(static_cast<unsigned>(64 * waves)), args, 0, s);
 }
 
 // Tile of the longest axis: 32, 64 or 80 rows (80 covers the 65-token
