@@ -2,7 +2,7 @@
 rocprofv3 counters.
 
   python -m vectra_amd.benchmarks.bandwidth_proof [--batches 64 1024] [--config serving] \\
-      [--out bandwidth.json] [--work gpurun_out/bandwidth]
+      [--out bandwidth.json] [--work rocprof_bandwidth]
 
 Restates the reference's benchmark/bandwidth/run_bandwidth_proof.py:16-120
 with rocprofv3 in place of Nsight Compute.  For each batch and for both the
@@ -160,7 +160,7 @@ def main(argv=None) -> int:
     p.add_argument('--config', default='serving', choices=sorted(configs.CONFIGS))
     p.add_argument('--batches', type=int, nargs='+', default=[64, UTILIZATION_BATCH])
     p.add_argument('--reps', type=int, default=20)
-    p.add_argument('--work', default='gpurun_out/bandwidth', help='rocprofv3 output directory')
+    p.add_argument('--work', default='rocprof_bandwidth', help='rocprofv3 output directory')
     p.add_argument('--out', default=None)
     args = p.parse_args(argv)
     os.makedirs(args.work, exist_ok=True)
