@@ -289,6 +289,8 @@ def main():
                      'peak': roofline.MI355X.hbm_bytes_per_s / 1e9, 'unit': 'GB/s'}
     line_roof['frac'] = line_roof['achieved'] / line_roof['peak']
     line_roof['kernel'] = KERNEL_NAMES.get(variant, variant)
+    if variant == 'plane' and config.dtype == torch.float32:
+        line_roof['kernel'] = 'rbf_plane32_kernel'  # the fp32 instantiation
     line_roof['traffic'] = None
     # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     # runs of this workload (profiles/traffic_<config>.json, made by

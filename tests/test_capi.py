@@ -84,12 +84,14 @@ def test_struct_layout_is_accepted():
         ({'d': 7, 'dv': 7}, 'generic'),
         ({'base': (1 << 20) + 2}, 'generic'),  # misaligned rows
         ({'n_q': 65, 'n_k': 65}, 'plane'),  # self-attention over a comparable set
-        ({'n_q': 65, 'n_k': 65, 'dtype': torch.float32}, 'mfma'),  # the same in fp32
+        ({'n_q': 65, 'n_k': 65, 'dtype': torch.float32}, 'plane'),  # the same in fp32
         ({'n_q': 65, 'n_k': 65, 'dtype': torch.float16, 'out_dtype': torch.float32}, 'plane'),
         ({'n_q': 65, 'n_k': 65, 'd': 16, 'dv': 16, 'contiguous': False}, 'plane'),  # model sites
         ({'n_q': 100, 'n_k': 100}, 'tile'),  # past one plane tile for 32-dim heads
         ({'n_q': 100, 'n_k': 100, 'd': 16, 'dv': 16}, 'plane'),  # 16-dim heads: tiles of 128
         ({'n_q': 200, 'n_k': 200, 'd': 16, 'dv': 16}, 'mfma'),  # 16-dim heads past 128 rows
+        ({'n_q': 100, 'n_k': 100, 'dtype': torch.float32}, 'mfma'),  # fp32 past one plane tile
+        ({'n_q': 65, 'n_k': 65, 'dtype': torch.float32, 'out_dtype': torch.bfloat16}, 'generic'),
         ({'n_q': 65, 'n_k': 65, 'd': 64, 'dv': 64}, 'tile'),
         ({'n_q': 4096, 'n_k': 4096, 'd': 64, 'dv': 64}, 'tile'),  # long key axis
         ({'n_q': 4096, 'n_k': 4096, 'd': 64, 'dv': 64, 'dtype': torch.float32}, 'mfma'),

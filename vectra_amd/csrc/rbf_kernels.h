@@ -24,9 +24,10 @@ hipError_t launch_generic(Problem& p, int in_dtype, int out_dtype, hipStream_t s
 bool mfma_supports(const Problem& p, int in_dtype, int out_dtype);
 hipError_t launch_mfma(Problem& p, int in_dtype, int out_dtype, hipStream_t s);
 
-// Plane kernel (one workgroup per (b, h) plane): bf16/fp16 inputs, output in the
-// input dtype or fp32, D == Dv in {16, 32}, Nq and Nk both <= 80 (<= 128 for
-// 16-dim heads), unit d stride, 16-byte-aligned rows.
+// Plane kernel (one workgroup per (b, h) plane): bf16/fp16/fp32 inputs, output
+// in the input dtype or fp32, D == Dv in {16, 32}, Nq and Nk both <= 80
+// (<= 128 for 16-dim heads), unit d stride, 16-byte-aligned rows, K and V
+// rows that do not overlap.
 bool plane_supports(const Problem& p, int in_dtype, int out_dtype);
 hipError_t launch_plane(Problem& p, int in_dtype, int out_dtype, hipStream_t s);
 
