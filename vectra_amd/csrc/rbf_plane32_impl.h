@@ -20,7 +20,10 @@
 //    they are, as fp32 (no 16-bit split); V^T sits in LDS with keys
 //    contiguous, so a lane's 4 keys of one value dim are one 16-byte read;
 //  * the weight sums are fp32 VALU adds (a lane's 4 keys per block) and two
-//    cross-lane steps at the end, not a product.
+//    cross-lane steps at the end, not a product;
+//  * key blocks past Nk are skipped, and up to 4 keys past the last whole
+//    block (65 keys: one) go through the VALU instead of a block of products
+//    that would be mostly padding.
 // Weights are used unshifted while a query's sum stays in [2^-100, 2^100]
 // (no fp32 overflow, and subnormal weights under 2^-20 of the sum); outside
 // that range (gamma < 0, a query far from every key, biases far from 0) the
@@ -210,7 +213,7 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
   float total[kPer];
 
   // The products of key block t for the first `n` query blocks.
-  auto block = [&](auto n_tag, int t, const float (&shift)[kPer]) {
+  auto block = [&](auto n_tag, int t, const float (&shift)[kPer]) __attribute__((always_inline)) {
     constexpr int n = decltype(n_tag)::value;
     float kf[kSteps];
 #pragma unroll
@@ -246,7 +249,48 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto pass = [&](auto n_tag, const float (&shift)[kPer]) {
+  // Keys past the last whole 16-key block, when there are at most 4 of them
+  // (65 keys: one), take the VALU instead of a block of products that would
+  // be mostly padding; key blocks past Nk are skipped (their weights are 0).
+  const int whole = n_k / 16;
+  const int tail = n_k - 16 * whole;
+  const bool valu_tail = tail > 0 && tail <= 4;
+  const int mfma_blocks = valu_tail ? whole : (n_k + 15) / 16;
+  // Score of tail key kt for query block j: the lane's dims, then the 4
+  // lanes of its query's column.
+  auto tail_score = [&](int j, int kt) __attribute__((always_inline)) {
+    const char* krow = k_lds + kt * G::kKStride + grp * kSteps * 4;
+    float part = 0.f;
+#pragma unroll
+    for (int c = 0; c < kSteps / 4; ++c) {
+      const float4 r = *reinterpret_cast<const float4*>(krow + 16 * c);
+      part = fmaf(r.x, qf[j][4 * c], part);
+      part = fmaf(r.y, qf[j][4 * c + 1], part);
+      part = fmaf(r.z, qf[j][4 * c + 2], part);
+      part = fmaf(r.w, qf[j][4 * c + 3], part);
+    }
+    return allreduce_bit32(allreduce_bit16(part, OpSum()), OpSum());
+  };
+  auto tail_key = [&](auto n_tag, int kt, const float (&shift)[kPer]) __attribute__((always_inline)) {
+    constexpr int n = decltype(n_tag)::value;
+    // This lane's value dims 16u + 4g + r of key kt.
+    float vk[G::kDTiles][4];
+#pragma unroll
+    for (int u = 0; u < G::kDTiles; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vk[u][r] = vt_lds[(16 * u + 4 * grp + r) * G::kVtStride + kt];
+    const float ck = c_lds[kt];
+#pragma unroll
+    for (int j = 0; j < n; ++j) {
+      const float wk = __builtin_amdgcn_exp2f(fmaf(coef, tail_score(j, kt), ck - shift[j]));
+      total[j] += grp == 0 ? wk : 0.f;  // the sum is reduced over the 4 lanes of a column
+#pragma unroll
+      for (int u = 0; u < G::kDTiles; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[j][u][r] = fmaf(wk, vk[u][r], acc[j][u][r]);
+    }
+  };
+  auto pass = [&](auto n_tag, const float (&shift)[kPer]) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
 #pragma unroll
@@ -254,16 +298,22 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
       total[j] = 0.f;
     }
 #pragma unroll
-    for (int t = 0; t < kNB; ++t) block(n_tag, t, shift);
+    for (int t = 0; t < kNB; ++t)
+      if (t < mfma_blocks) block(n_tag, t, shift);
+    if (valu_tail)
+      for (int kt = 16 * whole; kt < n_k; ++kt) tail_key(n_tag, kt, shift);
     // A query's sum: its lane's keys, then the 4 lanes of its column.
 #pragma unroll
     for (int j = 0; j < kPer; ++j) total[j] = allreduce_bit32(allreduce_bit16(total[j], OpSum()), OpSum());
   };
   // Each query's exact maximum logit in block j (the rare second pass).
-  auto row_max = [&](int j) {
+  auto row_max = [&](int j) __attribute__((always_inline)) {
     float rmax = -INFINITY;
+    if (valu_tail)
+      for (int kt = 16 * whole; kt < n_k; ++kt) rmax = fmaxf(rmax, fmaf(coef, tail_score(j, kt), c_lds[kt]));
 #pragma unroll
     for (int t = 0; t < kNB; ++t) {
+      if (t >= mfma_blocks) continue;
       float kf[kSteps];
 #pragma unroll
       for (int c = 0; c < kSteps / 4; ++c) {
@@ -306,6 +356,8 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
   }
 
   char* out_plane = static_cast<char*>(p.out) + (b * p.so[0] + h * p.so[1]) * static_cast<int64_t>(4);
+
+
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int32_t out_q = 16 * (first_block + j) + col;
