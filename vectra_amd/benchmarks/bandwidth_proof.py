@@ -29,7 +29,9 @@ reference reads from its serving SLO:
   exceeds the caches (1024), where it measures streaming, not launch latency.
 
 The analytic budgets of `vectra_amd.benchmarks.roofline` are reported
-beside the counters.  Exits 1 when a gate fails.
+beside the counters, and with `--read-ceiling` so is a plain read of the
+fused bytes measured the same way (`eager_gpu --impl read`): what the
+hardware itself reaches with one call at a time.  Exits 1 when a gate fails.
 """
 
 import argparse
@@ -162,19 +164,26 @@ def main(argv=None) -> int:
     p.add_argument('--reps', type=int, default=20)
     p.add_argument('--work', default='rocprof_bandwidth', help='rocprofv3 output directory')
     p.add_argument('--out', default=None)
+    p.add_argument('--read-ceiling', action='store_true',
+                   help='also profile a plain read of the fused bytes, reported beside the gates')
     args = p.parse_args(argv)
     os.makedirs(args.work, exist_ok=True)
     work = os.path.abspath(args.work)
     config = configs.CONFIGS[args.config]
     scales = copy_scales(work)
     measured, budgets = {}, {}
+    ceilings = {}
     for batch in args.batches:
         measured[batch] = {impl: measure(args.config, batch, impl, work, scales, args.reps)
                            for impl in ('eager', 'fused')}
+        if args.read_ceiling:
+            ceilings[batch] = measure(args.config, batch, 'read', work, scales, args.reps)
         budgets[batch] = roofline.analyze(dataclasses.replace(config, batch=batch).shape())
     failures = evaluate(measured)
     report = {'config': args.config, 'copy_scales': scales, 'measured': measured,
               'analytic_budgets': budgets, 'failures': failures, 'passed': not failures}
+    if ceilings:
+        report['read_ceiling'] = ceilings
     text = json.dumps(report, indent=2)
     if args.out:
         with open(args.out, 'w', encoding='utf-8') as f:

@@ -1,6 +1,6 @@
 """The eager operator chain on the GPU, beside the fused operator.
 
-  python -m vectra_amd.benchmarks.eager_gpu --impl eager|fused [--config serving] [--batch B] [--reps 20]
+  python -m vectra_amd.benchmarks.eager_gpu --impl eager|fused|read [--config serving] [--batch B] [--reps 20]
 
 `eager_rbf_attention` restates the reference's eager chain
 (kernels/vectra_kernels/reference.py:46-58): the [B, H, Lq, Lk, D]
@@ -8,6 +8,9 @@ difference, its square and sum, `-d * scale (+ bias)`, softmax and the
 product with v, each a separate kernel.  For 16-bit inputs the coefficient
 is cast to the input dtype first, as the reference's benchmarks do
 (kernels/benchmarks/throughput.py:129-131), so the chain stays in that dtype.
+
+`--impl read` is a plain HBM read of the fused operator's algorithmic
+bytes instead: the ceiling the hardware reaches under the same timing.
 
 The script runs the chosen implementation `--reps` times over rotating input
 sets (after one warm-up call per set) and prints one JSON line with the
@@ -48,20 +51,43 @@ def fused(q, k, v, scale, key_bias=None):
 IMPLS = {'eager': eager_rbf_attention, 'fused': fused}
 
 
+def read_region(config, batch, n_sets):
+    """A plain HBM read of the fused operator's algorithmic bytes (the
+    hardware's ceiling under the same one-call-at-a-time timing), one buffer
+    per input set.  Buffers and the sink are built on the host and copied, so
+    the only kernel of a call is the read."""
+    from vectra_amd.benchmarks import read_ceiling  # pylint: disable=import-outside-toplevel
+    from vectra_amd.benchmarks import roofline  # pylint: disable=import-outside-toplevel
+    import dataclasses  # pylint: disable=import-outside-toplevel
+
+    nbytes = roofline.fused_bytes(dataclasses.replace(config, batch=batch or config.batch).shape())
+    nbytes = (nbytes + 15) // 16 * 16
+    gen = torch.Generator().manual_seed(0)
+    bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, generator=gen).to('cuda') for _ in range(n_sets)]
+    blocks = torch.cuda.get_device_properties(0).multi_processor_count * 8
+    sink = torch.zeros(blocks * read_ceiling.THREADS, dtype=torch.int32).to('cuda')
+    stream = torch.cuda.current_stream()
+    return [lambda b=b: read_ceiling.read_once(b, sink, blocks, stream) for b in bufs]
+
+
 def main():
     p = argparse.ArgumentParser()
-    p.add_argument('--impl', choices=sorted(IMPLS), required=True)
+    p.add_argument('--impl', choices=sorted(IMPLS) + ['read'], required=True)
     p.add_argument('--config', default='serving', choices=sorted(configs.CONFIGS))
     p.add_argument('--sets', type=int, default=5)
     p.add_argument('--reps', type=int, default=20)
     p.add_argument('--batch', type=int, default=None, help='first B batch entries of the config (default: all)')
     args = p.parse_args()
     config = configs.CONFIGS[args.config]
-    fn = IMPLS[args.impl]
-    sets = [configs.make_inputs(config, seed=s, batch=args.batch).to('cuda') for s in range(args.sets)]
+    if args.impl == 'read':
+        calls_of_set = read_region(config, args.batch, args.sets)
+    else:
+        fn = IMPLS[args.impl]
+        sets = [configs.make_inputs(config, seed=s, batch=args.batch).to('cuda') for s in range(args.sets)]
+        calls_of_set = [lambda s=s: fn(*s.args()) for s in sets]
     calls = 0
-    for s in sets:
-        fn(*s.args())
+    for call in calls_of_set:
+        call()
         calls += 1
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
@@ -69,7 +95,7 @@ def main():
     for i in range(args.reps):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
-        fn(*sets[i % args.sets].args())
+        calls_of_set[i % args.sets]()
         end.record(stream)
         end.synchronize()
         calls += 1
