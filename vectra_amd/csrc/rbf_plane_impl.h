@@ -165,7 +165,10 @@ struct PlaneGeo {
 constexpr int kPlaneBlocksPerWave = 2;
 
 template <typename T, typename OutT, int kD, int kKeys>
-__global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane_kernel(Problem p) {
+// 16-dim heads over at most 80 keys fit 8 waves per SIMD (64 VGPRs) with no
+// spills; more resident workgroups keep more of HBM's latency covered.
+__global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2))
+__attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_plane_kernel(Problem p) {
   using G = PlaneGeo<T, kD, kKeys>;
   using Ops = MfmaOps<T>;
   using Frag = typename G::Frag;
