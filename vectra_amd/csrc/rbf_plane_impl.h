@@ -164,9 +164,9 @@ struct PlaneGeo {
 // instructions).
 constexpr int kPlaneBlocksPerWave = 2;
 
-template <typename T, typename OutT, int kD, int kKeys>
 // 16-dim heads over at most 80 keys fit 8 waves per SIMD (64 VGPRs) with no
 // spills; more resident workgroups keep more of HBM's latency covered.
+template <typename T, typename OutT, int kD, int kKeys>
 __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2))
 __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_plane_kernel(Problem p) {
   using G = PlaneGeo<T, kD, kKeys>;
@@ -236,7 +236,7 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
   // hardware), with one per-lane offset computed once and per-round parts in
   // scalar registers.  Piece i of K is row i / kChunks, 16-byte chunk
   // i % kChunks; V pair slot i is rows 2 (i / kChunks) and + 1 of the same
-  // chunk.  No row offset reaches 2^32 (the host checks (kKeys + 1) rows).
+  // chunk.  No row offset reaches 2^32 (the host checks 144 rows of each stride).
   const char* kp = static_cast<const char*>(p.k) + (b * p.sk[0] + h * p.sk[1]) * 2;
   const char* vp = static_cast<const char*>(p.v) + (b * p.sv[0] + h * p.sv[1]) * 2;
   const char* qp = static_cast<const char*>(p.q) + (b * p.sq[0] + h * p.sq[1]) * 2;
