@@ -565,3 +565,35 @@ def test_offsets_beyond_32_bits():
         np.testing.assert_allclose(got, want, err_msg=f'far planes {variant}', **HALF_TOL)
     del far_planes
     torch.cuda.empty_cache()
+
+
+# fp32 planes: key counts with 0-4 keys past a whole 16-key block (those keys
+# take the VALU in the fp32 plane kernel, key blocks past Nk are skipped) and
+# more than 4 (a block of products), with and without a masked tail key.
+FP32_TAIL_CASES = [(n_q, n_k, dim) for n_q in (16, 65) for n_k in (1, 2, 4, 5, 17, 20, 33, 36, 64, 65, 68)
+                   for dim in (16, 32)]
+
+
+@pytest.mark.parametrize('shape', FP32_TAIL_CASES, ids=str)
+def test_fp32_plane_tail_keys(shape):
+    n_q, n_k, dim = shape
+    gen = torch.Generator().manual_seed(31 + n_k + 7 * n_q + dim)
+    q = torch.randn(2, 3, n_q, dim, generator=gen)
+    k = torch.randn(2, 3, n_k, dim, generator=gen)
+    v = torch.randn(2, 3, n_k, dim, generator=gen)
+    scale = torch.full((1, 3, 1, 1), 1.0 / dim)
+    bias = torch.zeros(2, 1, 1, n_k)
+    if n_k > 1:
+        bias[1, ..., n_k - 1] = -math.inf  # the last (tail) key masked in one batch entry
+        bias[0, ..., 0] = 0.75
+    variants = _variants(q, k, v, scale, bias)
+    assert 'plane' in variants, variants
+    print(f'shape={shape}', flush=True)
+    _check(q, k, v, scale, bias)
+    # Negative gamma (the shifted second pass, tail keys included) and a
+    # fully masked row.
+    _check(q, k, v, -scale, bias)
+    masked = bias.clone()
+    masked[0] = -math.inf
+    got = run(q, k, v, scale, masked, 'plane')
+    assert torch.isnan(got[0]).all() and torch.isfinite(got[1]).all()
