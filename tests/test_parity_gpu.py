@@ -597,3 +597,67 @@ def test_fp32_plane_tail_keys(shape):
     masked[0] = -math.inf
     got = run(q, k, v, scale, masked, 'plane')
     assert torch.isnan(got[0]).all() and torch.isfinite(got[1]).all()
+
+
+# Preallocated outputs under strides the operator's callers hand in: heads
+# inside rows (a [B, Nq, H, Dv] buffer viewed as [B, H, Nq, Dv]), every other
+# element, and rows one element longer than Dv (unaligned rows).
+OUT_LAYOUTS = ('heads_inner', 'every_other', 'odd_rows')
+OUT_LAYOUT_SHAPES = [(1, 64, 32, torch.bfloat16), (65, 65, 16, torch.bfloat16), (65, 65, 32, torch.float16),
+                     (65, 65, 32, torch.float32), (40, 200, 32, torch.bfloat16), (40, 100, 64, torch.float32),
+                     (20, 70, 128, torch.bfloat16), (20, 70, 48, torch.bfloat16)]
+
+
+def _out_view(layout, b, h, n_q, dv, dtype, sentinel):
+    if layout == 'heads_inner':
+        buf = torch.full((b, n_q, h, dv), sentinel, dtype=dtype, device='cuda')
+        return buf, buf.permute(0, 2, 1, 3)
+    if layout == 'every_other':
+        buf = torch.full((b, h, n_q, 2 * dv), sentinel, dtype=dtype, device='cuda')
+        return buf, buf[..., ::2]
+    buf = torch.full((b, h, n_q, dv + 1), sentinel, dtype=dtype, device='cuda')
+    return buf, buf[..., :dv]
+
+
+@pytest.mark.parametrize('layout', OUT_LAYOUTS)
+@pytest.mark.parametrize('shape', OUT_LAYOUT_SHAPES, ids=str)
+def test_preallocated_strided_outputs(shape, layout):
+    """Every variant that accepts the output view writes exactly the values
+    it writes into a contiguous output, and nothing outside the view."""
+    n_q, n_k, dim, dtype = shape
+    gen = torch.Generator().manual_seed(41 + n_q + n_k + dim)
+    b, h = 3, 4
+    q = torch.randn(b, h, n_q, dim, generator=gen).to(dtype).cuda()
+    k = torch.randn(b, h, n_k, dim, generator=gen).to(dtype).cuda()
+    v = torch.randn(b, h, n_k, dim, generator=gen).to(dtype).cuda()
+    scale = torch.full((1, h, 1, 1), 1.0 / dim, device='cuda')
+    bias = torch.zeros(b, 1, 1, n_k, device='cuda')
+    for i in range(b):
+        bias[i, ..., n_k - i:] = -math.inf  # ragged key counts
+    bias[0, ..., 0] = 0.5
+    scale4, bias4 = capi.broadcast_operands(q, k, scale, bias)
+    sentinel = 7.0
+    checked = set()
+    for out_dtype in {torch.float32, dtype}:
+        buf, view = _out_view(layout, b, h, n_q, dim, out_dtype, sentinel)
+        for variant in ('auto', 'generic', 'stream', 'mfma', 'plane', 'tile'):
+            chosen = capi.select_variant(capi.make_args(q, k, v, view, scale4, bias4, variant))
+            if chosen <= 0:
+                continue
+            checked.add(variant)
+            print(f'shape={shape} layout={layout} out={out_dtype} variant={variant}', flush=True)
+            buf.fill_(sentinel)
+            # 'auto' against the kernel it picks for this view (a contiguous
+            # output may pick another one).
+            want = capi.forward(q, k, v, scale, bias, out_dtype=out_dtype, variant=capi.VARIANT_NAMES[chosen])
+            capi.forward(q, k, v, scale, bias, out=view, variant=variant)
+            torch.cuda.synchronize()
+            assert torch.equal(view, want), variant
+            rest = buf.clone()
+            rest.as_strided(view.shape, view.stride()).fill_(sentinel)
+            assert rest.eq(sentinel).all(), f'{variant} wrote outside the view'
+    # Query blocks of 16-, 32-, 64- and 128-dim heads reach a matrix-core
+    # kernel under every layout; single queries reach the stream kernel only
+    # under 16-byte aligned rows.
+    if (n_q >= 16 and dim != 48) or (layout == 'heads_inner' and n_q == 1):
+        assert checked - {'auto', 'generic'}, checked
