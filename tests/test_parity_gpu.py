@@ -453,9 +453,21 @@ def test_squared_norms():
         np.testing.assert_allclose(got.double().numpy(), want.numpy(), rtol=1e-5, atol=1e-5)
 
 
-def test_graph_replays_match_eager():
-    inputs = configs.make_inputs(configs.SERVING, seed=4, batch=256).to('cuda')
+GRAPH_CASES = [(configs.SERVING, 256, 'stream'), (configs.SELF_ATTENTION, 64, 'plane'),
+               (configs.SELF_ATTENTION.with_dtype(torch.float32), 64, 'plane'), (configs.LONG_KEY, 1, 'tile')]
+
+
+@pytest.mark.parametrize('config,batch,kernel', GRAPH_CASES,
+                         ids=lambda c: f'{c.name}-{c.dtype}'.replace('torch.', '') if hasattr(c, 'name') else str(c))
+def test_graph_replays_match_eager(config, batch, kernel):
+    """Graph replays of the operator (the stream, plane, fp32 plane and tile
+    kernels) give the eager result on every replay."""
+    inputs = configs.make_inputs(config, seed=4, batch=batch).to('cuda')
     eager = torch.ops.vectra.rbf_attention(*inputs.args())
+    q, k, v, scale, bias = inputs.args()
+    scale4, bias4 = capi.broadcast_operands(q, k, scale, bias)
+    chosen = capi.select_variant(capi.make_args(q, k, v, eager, scale4, bias4, 'auto'))
+    assert capi.VARIANT_NAMES[chosen] == kernel
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
