@@ -162,3 +162,35 @@ def test_squared_norms_validates_on_the_host():
     assert lib.vectra_rbf_squared_norms(None, 0, 1, -1, 1, 1, strides, None, None) == capi.ERR_BAD_SHAPE
     assert lib.vectra_rbf_squared_norms(None, 0, 0, 1, 1, 1, strides, None, None) == capi.OK
     assert lib.vectra_rbf_squared_norms(None, 0, 1, 1, 1, 1, strides, None, None) == capi.ERR_NULL_ARGUMENT
+
+
+
+_MISSING_SCRIPT = r'''
+import importlib
+for module in ('vectra_amd.kernels', 'vectra_amd.kernels.capi'):
+    try:
+        importlib.import_module(module)
+        print(module, 'imported')
+    except ImportError as e:
+        print(module, type(e).__name__, e)
+'''
+
+
+def test_a_missing_library_fails_loudly(tmp_path):
+    """A copy of the Python package without the built libraries: neither the
+    operator nor the C-ABI bindings import, so there is no CPU fallback to
+    land on."""
+    import shutil
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    shutil.copytree(os.path.join(root, 'vectra_amd'), tmp_path / 'vectra_amd',
+                    ignore=shutil.ignore_patterns('lib', 'csrc', '__pycache__'))
+    done = subprocess.run([sys.executable, '-c', _MISSING_SCRIPT], cwd=tmp_path, capture_output=True, text=True,
+                          timeout=300, env=dict(os.environ, PYTHONPATH=str(tmp_path)))
+    assert done.returncode == 0, done.stderr
+    lines = done.stdout.strip().splitlines()
+    assert len(lines) == 2, lines
+    for line in lines:
+        assert ' NativeLibraryMissing ' in line, line
+        assert 'libvectra_torch.so is missing' in line and 'make -C vectra_amd/csrc' in line, line
