@@ -13,9 +13,11 @@ kernel must match the eager chain (the CPU baseline below) within rtol 1e-3 /
 atol 1e-4 (bf16/fp16 inputs) or 1e-5 / 1e-6 (fp32), and the operator's
 v.dtype output must be exactly that fp32 result rounded once.
 
-The K timed steps are one HIP-graph replay of K operator launches (host
-launch overhead is not the GPU's throughput), bracketed by
-torch.cuda.synchronize() and events on the stream the kernels run on.
+The K timed steps are HIP-graph replays of trials of up to 100 operator
+launches (host launch overhead is not the GPU's throughput), bracketed by
+torch.cuda.synchronize() and events on the stream the kernels run on; the
+first trial is queued behind an untimed lead-in replay, so no trial starts
+on an idle GPU (see time_trials).
 
 Prints one JSON line:  queries/s (value), ms_per_step, the roofline of the
 kernel (algorithmic bytes / average launch time vs 8 TB/s) and the CPU
@@ -164,12 +166,25 @@ def cpu_baseline(config, host_inputs, seconds):
 TRIAL_STEPS = 100
 
 
+# Launches of the lead-in replay that runs, unsynchronised, right before the
+# first timed trial (about 0.8 ms of GPU work at the serving shape).
+LEAD_STEPS = 64
+
+
 def time_trials(step, steps, warmup, stream, graph=True):
     """Milliseconds per step of each trial of the K = `steps` timed launches.
 
     Each trial is one HIP-graph replay of its launches (or a host loop with
     graph=False), bracketed by events on `stream`, the stream the kernels run
     on; the K launches are bracketed by synchronisations on both sides.
+
+    With graphs, the W warm-up launches run as one replay, then the device is
+    synchronised, then a lead-in replay of max(W, LEAD_STEPS) launches is
+    queued and the first trial's start event is recorded straight behind it
+    with no synchronisation between.  The host submits the timed replay while
+    the lead-in still runs, so the start event does not fire on an idle GPU
+    and the host's graph-launch latency stays outside the timed region (a
+    trial that starts on an idle GPU times that latency as well).
     """
     sizes = [TRIAL_STEPS] * (steps // TRIAL_STEPS) + ([steps % TRIAL_STEPS] if steps % TRIAL_STEPS else [])
     if graph:
@@ -185,16 +200,22 @@ def time_trials(step, steps, warmup, stream, graph=True):
         with torch.cuda.graph(warm):
             for i in range(max(warmup, 1)):
                 step(i)
+        lead = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(lead):
+            for i in range(max(warmup, LEAD_STEPS)):
+                step(i)
         for size in set(sizes):
             graphs[size] = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graphs[size]):
                 for i in range(size):
                     step(i)
         warm.replay()
+        torch.cuda.synchronize()
+        lead.replay()  # no synchronisation: the timed replays queue behind it
     else:
         for i in range(warmup):
             step(i)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
     events = []
     for size in sizes:
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

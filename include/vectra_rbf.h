@@ -10,12 +10,18 @@
  *   the Triton launch) and
  *   kernels/vectra_kernels/norm_precompute.py:67-86 (squared_norms),
  * which the reference binds to the operator at
- *   kernels/vectra_kernels/custom_ops.py:93-103 (the 'cuda' kernel registration).
+ *   kernels/vectra_kernels/custom_ops.py:75-85 (the 'cuda' kernel registration).
  *
  * Contract:
  *  - Plain pointers, sizes and element strides; no torch types cross the ABI.
  *  - Every buffer is owned by the caller.  The library allocates nothing on
- *    the device or the host and keeps no mutable global state, so calls are
+ *    the device or the host.  Its only global state is three write-once
+ *    caches of facts that never change within a process: the compute-unit
+ *    count of each device (an atomic per device id), the environment
+ *    override VECTRA_STREAM_WAVES_PER_CU (read once), and per kernel
+ *    instantiation the number of its workgroups resident on one compute
+ *    unit (an atomic, asked of the HIP runtime on first launch).  Two threads
+ *    that fill one cache at once store the same value, so calls are
  *    reentrant and may be captured into a HIP graph.
  *  - Work is enqueued on `stream` and the call returns without synchronising.
  *  - Errors are returned as a status code (never thrown); see
@@ -113,7 +119,9 @@ typedef struct vectra_rbf_args {
  * Replaces spatial_rbf_attention.py:177-281 (host launch) and :47-174 (kernel).
  * Returns VECTRA_OK or an error code; on error nothing was enqueued.
  * Zero-sized problems (B*H*Nq == 0 or Dv == 0) are a successful no-op;
- * Nk == 0 with Nq > 0 writes NaN rows, as softmax over an empty set does.
+ * Nk == 0 with Nq > 0 writes rows of zeros, as the reference's default
+ * implementation does (reference.py:79-99: softmax over an empty axis times
+ * an empty v is an empty sum, 0).
  */
 int vectra_rbf_attention_fwd(const vectra_rbf_args* args, vectra_stream_t stream);
 

@@ -5,7 +5,7 @@ The reference ships no golden vectors for this path (its numerics tests draw
 seeded inputs at run time and compare with its float64 oracle,
 kernels/tests/test_parity.py:49-98).  These fixtures are computed here by
 the most literal reading of the operator's definition
-(kernels/vectra_kernels/custom_ops.py:78-89), independent of oracle/: pure
+(kernels/vectra_kernels/custom_ops.py:52-72; reference.py:46-58), independent of oracle/: pure
 Python float64 loops over b, h, i, j, d with math.exp, an explicit
 maximum subtraction, NaN for a row whose keys are all masked, and zeros for an
 empty key set.

@@ -119,6 +119,46 @@ def test_plane_kernel_needs_disjoint_rows_within_32_bit_offsets():
     assert capi.VARIANT_NAMES[capi.select_variant(a)] != 'plane'
 
 
+@pytest.mark.parametrize('n,variant', [(65, 'plane'), (100, 'tile')])
+def test_output_views_past_4_gib_of_a_plane_go_to_64_bit_kernels(n, variant):
+    """The plane and tile kernels store through 32-bit byte offsets from a
+    plane's first output element, so they take a strided output only while
+    its last element lies within 4 GiB of the first: at 2^30 elements for an
+    fp32 output, 2^31 for a 16-bit one.  Larger views go to a kernel with
+    64-bit addressing."""
+    h, dv = 8, 32
+
+    def with_out_rows(row, out_dtype):
+        a = _fake_args(n_q=n, n_k=n, out_dtype=out_dtype)
+        a.out_stride = (ctypes.c_int64 * 4)(h * n * row, n * row, row, 1)
+        return capi.VARIANT_NAMES[capi.select_variant(a)]
+
+    # Last element offset (n - 1) * row + dv - 1, in elements.
+    fits_f32 = (((1 << 30) - dv) // (n - 1))  # below 2^30 elements
+    past_f32 = -(-((1 << 30) - dv + 1) // (n - 1))  # at or past 2^30 elements
+    assert (n - 1) * fits_f32 + dv - 1 < (1 << 30) <= (n - 1) * past_f32 + dv - 1
+    assert with_out_rows(fits_f32, torch.float32) == variant
+    assert with_out_rows(past_f32, torch.float32) not in ('plane', 'tile')
+    assert with_out_rows(past_f32, torch.bfloat16) == variant  # 2-byte elements: 2^31
+    past_16 = -(-((1 << 31) - dv + 1) // (n - 1))
+    assert with_out_rows(past_16, torch.bfloat16) not in ('plane', 'tile')
+
+
+def test_sizes_beyond_the_kernels_index_range_are_rejected():
+    for field, value in (('batch', 1 << 31), ('n_k', 1 << 40), ('value_dim', 1 << 31)):
+        a = _fake_args()
+        setattr(a, field, value)
+        assert capi.select_variant(a) == -capi.ERR_TOO_LARGE, field
+    a = _fake_args(d=1 << 24, dv=(65535 * 256) + 1)  # one more 256-column slice than the grid holds
+    assert capi.select_variant(a) == -capi.ERR_TOO_LARGE
+    a = _fake_args(b=1 << 12, h=1 << 12, n_q=1 << 8)  # 2^32 rows
+    assert capi.select_variant(a) == -capi.ERR_TOO_LARGE
+    lib = _native.hip_library()
+    strides = (ctypes.c_int64 * 4)(0, 0, 0, 1)
+    big = 1 << 40
+    assert lib.vectra_rbf_squared_norms(1, 0, big, big, 2, 1, strides, 1, None) == capi.ERR_TOO_LARGE
+
+
 def test_forcing_a_variant_that_cannot_run_is_an_error():
     a = _fake_args(d=24, dv=24, variant='stream')
     assert capi.select_variant(a) == -capi.ERR_BAD_VARIANT

@@ -109,6 +109,32 @@ def test_bias_broadcasts(bias_shape):
                                rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize('scale_dtype,bias_dtype', [(torch.int32, torch.bool), (torch.int64, torch.int8),
+                                                     (torch.uint8, torch.int32)])
+def test_integer_and_bool_coefficients_are_read_as_float32(scale_dtype, bias_dtype):
+    """The reference converts the coefficient and the bias with
+    .to(torch.float32) (spatial_rbf_attention.py:208-213, :221), so an integer
+    coefficient and a bool or integer bias are accepted and mean their fp32
+    values."""
+    q, k, v, _, _ = _inputs()
+    scale = torch.tensor([[[[1]], [[0]], [[2]]]], dtype=scale_dtype) if scale_dtype != torch.uint8 \
+        else torch.tensor(1, dtype=scale_dtype)
+    gen = torch.Generator().manual_seed(2)
+    bias = (torch.rand(2, 1, 1, 9, generator=gen) * 3).to(bias_dtype)
+    out = torch.ops.vectra.rbf_attention(q, k, v, scale, bias)
+    assert torch.equal(out, torch.ops.vectra.rbf_attention(q, k, v, scale.float(), bias.float()))
+    # gamma up to 2 over 16 dims: the expansion's cancellation error in fp32
+    # is ~20x that of the other CPU tests' gamma <= 0.12.
+    want = oracle.expanded_fp64(q, k, v, scale.float(), bias.float())
+    np.testing.assert_allclose(out.double().numpy(), want, rtol=2e-4, atol=1e-5)
+
+
+def test_complex_coefficient_raises():
+    q, k, v, _, bias = _inputs()
+    with pytest.raises(RuntimeError, match='must be real'):
+        torch.ops.vectra.rbf_attention(q, k, v, torch.tensor(0.1 + 0j), bias)
+
+
 def test_per_query_bias_is_a_value_error():
     q, k, v, scale, _ = _inputs()
     with pytest.raises(ValueError, match='constant across queries'):

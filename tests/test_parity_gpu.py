@@ -611,6 +611,28 @@ def test_fp32_plane_tail_keys(shape):
     assert torch.isnan(got[0]).all() and torch.isfinite(got[1]).all()
 
 
+def test_fp32_plane_large_values_do_not_overflow():
+    """Queries on top of keys with gamma*|q|^2 = 60: the fp32 plane kernel's
+    unshifted weight for the matching key is e^60 (about 2^87), and with
+    |v| near 2^50 the unshifted value products would pass fp32's 2^128.  The
+    kernel must take its max-subtracted pass for such queries and return v of
+    the matching key, as the float64 oracle does."""
+    gen = torch.Generator().manual_seed(53)
+    b, h, n, dim = 2, 3, 65, 32
+    gamma = 1.0 / dim
+    k = torch.randn(b, h, n, dim, generator=gen, dtype=torch.float64)
+    k = k / k.norm(dim=-1, keepdim=True) * math.sqrt(60.0 / gamma)
+    k = k.float()
+    q = k.clone()
+    v = (torch.randn(b, h, n, dim, generator=gen) * 2.0 ** 50).float()
+    scale = torch.full((1, h, 1, 1), gamma)
+    assert 'plane' in _variants(q, k, v, scale, None)
+    got = run(q, k, v, scale, None, 'plane').double()
+    assert torch.isfinite(got).all()
+    want = oracle.direct_fp64(q, k, v, scale)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-5, atol=0)
+
+
 # Preallocated outputs under strides the operator's callers hand in: heads
 # inside rows (a [B, Nq, H, Dv] buffer viewed as [B, H, Nq, Dv]), every other
 # element, and rows one element longer than Dv (unaligned rows).

@@ -1,6 +1,6 @@
 // torch.library registration of vectra::rbf_attention for PyTorch-ROCm.
 //
-// Mirrors the reference operator kernels/vectra_kernels/custom_ops.py:70-115:
+// Mirrors the reference operator kernels/vectra_kernels/custom_ops.py:52-97 (op and schema :52-72, 'cuda' kernel :75-85):
 //   schema  rbf_attention(Tensor q, Tensor k, Tensor v, Tensor scale,
 //                         Tensor? key_bias=None) -> Tensor
 //   CUDA key (HIP tensors on ROCm)  -> libvectra_rbf.so (include/vectra_rbf.h),
@@ -44,8 +44,20 @@ struct Inputs {
   at::Tensor bias;   // expanded view [B, H, 1, Nk] or undefined
 };
 
+// The coefficient and the bias are read in their own dtype when the kernels
+// decode it (fp32, fp16, bf16, fp64).  Any other real dtype (integers, bool,
+// 8-bit floats) is converted to fp32 first, as the reference converts both
+// with `.to(torch.float32)` (spatial_rbf_attention.py:208-213, :221;
+// reference.py:43, :98).
+at::Tensor readable_coefficient(const at::Tensor& t, const char* name) {
+  if (to_vectra_dtype(t.scalar_type()) >= 0) return t;
+  TORCH_CHECK(!at::isComplexType(t.scalar_type()), "vectra::rbf_attention: ", name,
+              " must be real; got ", t.scalar_type());
+  return t.to(at::kFloat);
+}
+
 Inputs check_inputs(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                    const at::Tensor& scale, const std::optional<at::Tensor>& key_bias) {
+                    const at::Tensor& scale_in, const std::optional<at::Tensor>& key_bias) {
   TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.dim() == 4,
               "vectra::rbf_attention: q, k and v must be 4-D [B, H, N, D]; got ", q.sizes(), ", ",
               k.sizes(), ", ", v.sizes());
@@ -68,15 +80,12 @@ Inputs check_inputs(const at::Tensor& q, const at::Tensor& k, const at::Tensor& 
   TORCH_CHECK(k.scalar_type() == dt && v.scalar_type() == dt,
               "vectra::rbf_attention: q, k and v must share a dtype; got ", dt, ", ",
               k.scalar_type(), ", ", v.scalar_type());
-  TORCH_CHECK(to_vectra_dtype(scale.scalar_type()) >= 0,
-              "vectra::rbf_attention: scale must be a floating tensor; got ", scale.scalar_type());
+  const at::Tensor scale = readable_coefficient(scale_in, "scale");
   TORCH_CHECK(scale.dim() <= 4, "vectra::rbf_attention: scale must broadcast to [B, H, 1, 1]");
   // Broadcasting rules and errors of Tensor.expand (spatial_rbf_attention.py:208-213).
   in.scale = scale.expand({in.B, in.H, 1, 1});
   if (key_bias.has_value() && key_bias->defined()) {
-    at::Tensor bias = *key_bias;
-    TORCH_CHECK(to_vectra_dtype(bias.scalar_type()) >= 0,
-                "vectra::rbf_attention: key_bias must be a floating tensor; got ", bias.scalar_type());
+    at::Tensor bias = readable_coefficient(*key_bias, "key_bias");
     TORCH_CHECK(bias.dim() <= 4, "vectra::rbf_attention: key_bias must broadcast to [B, H, 1, Nk]");
     while (bias.dim() < 4) bias = bias.unsqueeze(0);
     // spatial_rbf_attention.py:224-225.
@@ -102,7 +111,8 @@ at::Tensor rbf_attention_hip(const at::Tensor& q, const at::Tensor& k, const at:
     // A CPU scalar coefficient is accepted, as elementwise ops accept it.
     TORCH_CHECK(scale_dev.device().is_cpu() && scale.numel() == 1,
                 "vectra::rbf_attention: scale must be on ", q.device(), " (or a CPU scalar)");
-    scale_dev = scale.reshape({1, 1, 1, 1}).to(q.device()).expand({in.B, in.H, 1, 1});
+    scale_dev = readable_coefficient(scale, "scale").reshape({1, 1, 1, 1}).to(q.device()).expand(
+        {in.B, in.H, 1, 1});
   }
   if (in.bias.defined())
     TORCH_CHECK(in.bias.device() == q.device(), "vectra::rbf_attention: key_bias must be on ",
@@ -153,7 +163,7 @@ at::Tensor rbf_attention_hip(const at::Tensor& q, const at::Tensor& k, const at:
 // ------------------------------------------------------------------- host
 //
 // The operator's implementation off the GPU (the reference's default
-// implementation, custom_ops.py:70-90): same expansion, clamp, masking and
+// implementation, custom_ops.py:52-72 calling reference.py:79-99): same expansion, clamp, masking and
 // fp32 accumulation as the device kernels, one task per query row.
 
 template <typename T>

@@ -4,7 +4,7 @@
 //                                  + key_bias[b,h,j]) * v[b,h,j,:]
 //
 // Semantics follow the reference operator (kernels/vectra_kernels/
-// spatial_rbf_attention.py:47-174 and custom_ops.py:70-115):
+// spatial_rbf_attention.py:47-174 and custom_ops.py:52-72):
 //  * distances by the Euclidean expansion with a clamp at zero (:137);
 //  * logits -scale*d plus the key bias; without a bias only keys < Nk count
 //    (:139-150);
@@ -363,15 +363,26 @@ void rbf_stream_kernel(Problem p) {
 // Generic kernel: one wave per (b, h, query row) and per 256-wide slice of
 // the value dimension (blockIdx.y).  Scores: lane = key within a 64-key
 // tile.  Value product: lane = value column, weights broadcast with
-// readlane.  Handles any strides (including zero), any D and Dv.
+// readlane.  Handles any strides (including zero), any D and Dv.  Waves
+// loop over rows with a grid stride, so the grid stays within HIP's
+// per-dimension thread limit however many rows there are.
 // ------------------------------------------------------------------------
 template <typename T, typename OutT>
-__global__ __launch_bounds__(256) void rbf_generic_kernel(Problem p) {
-  constexpr int kCols = 4;  // value columns per lane: 4 * 64 = 256 per slice
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row_id = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row_id >= p.total_rows) return;  // no barriers below
+__device__ void generic_row(const Problem& p, int64_t row_id, int lane);
 
+template <typename T, typename OutT>
+__global__ __launch_bounds__(256) void rbf_generic_kernel(Problem p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 4;
+  // Wave-uniform loop (no barriers inside).
+  for (int64_t row_id = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row_id < p.total_rows;
+       row_id += stride)
+    generic_row<T, OutT>(p, row_id, lane);
+}
+
+template <typename T, typename OutT>
+__device__ void generic_row(const Problem& p, int64_t row_id, int lane) {
+  constexpr int kCols = 4;  // value columns per lane: 4 * 64 = 256 per slice
   const int64_t i = row_id % p.Nq;
   const int64_t bh = row_id / p.Nq;
   const int64_t h = bh % p.H;
@@ -451,19 +462,22 @@ struct NormArgs {
   int64_t s[4];
 };
 
+// Threads loop over rows with a grid stride.
 template <typename T>
 __global__ __launch_bounds__(256) void squared_norms_kernel(NormArgs a) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (r >= a.B * a.H * a.N) return;
-  const int64_t n = r % a.N;
-  const int64_t bh = r / a.N;
-  const T* row = static_cast<const T*>(a.x) + (bh / a.H) * a.s[0] + (bh % a.H) * a.s[1] + n * a.s[2];
-  float acc = 0.f;
-  for (int64_t d = 0; d < a.D; ++d) {
-    const float t = to_float<T>(row[d * a.s[3]]);
-    acc += t * t;
+  const int64_t total = a.B * a.H * a.N;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; r < total; r += stride) {
+    const int64_t n = r % a.N;
+    const int64_t bh = r / a.N;
+    const T* row = static_cast<const T*>(a.x) + (bh / a.H) * a.s[0] + (bh % a.H) * a.s[1] + n * a.s[2];
+    float acc = 0.f;
+    for (int64_t d = 0; d < a.D; ++d) {
+      const float t = to_float<T>(row[d * a.s[3]]);
+      acc += t * t;
+    }
+    a.out[r] = acc;
   }
-  a.out[r] = acc;
 }
 
 // ------------------------------------------------------------------------
@@ -516,10 +530,16 @@ static hipError_t launch_stream_t(Problem& p, int chunks, hipStream_t s) {
   }
 }
 
+// Workgroups of the grid-stride kernels: at most this many (of 256 threads).
+constexpr int64_t kMaxGridStrideBlocks = int64_t{1} << 20;
+
 template <typename T, typename OutT>
 static hipError_t launch_generic_t(Problem& p, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((p.total_rows + 3) / 4),
-                  static_cast<unsigned>((p.Dv + 255) / 256));
+  const int64_t blocks = (p.total_rows + 3) / 4;
+  const int64_t slices = (p.Dv + 255) / 256;
+  if (slices > kMaxGenericSlices) return hipErrorInvalidValue;  // the host rejects these first
+  const dim3 grid(static_cast<unsigned>(blocks < kMaxGridStrideBlocks ? blocks : kMaxGridStrideBlocks),
+                  static_cast<unsigned>(slices));
   return launch(reinterpret_cast<const void*>(&rbf_generic_kernel<T, OutT>), grid, dim3(256), p, s);
 }
 
@@ -565,7 +585,8 @@ hipError_t launch_generic(Problem& p, int in_dt, int out_dt, hipStream_t s) {
 hipError_t launch_squared_norms(const void* x, int dtype, int64_t B, int64_t H, int64_t N,
                                 int64_t D, const int64_t* st, float* out, hipStream_t s) {
   NormArgs a{x, out, B, H, N, D, {st[0], st[1], st[2], st[3]}};
-  const dim3 grid(static_cast<unsigned>((B * H * N + 255) / 256));
+  const int64_t blocks = (B * H * N + 255) / 256;
+  const dim3 grid(static_cast<unsigned>(blocks < kMaxGridStrideBlocks ? blocks : kMaxGridStrideBlocks));
   void* args[] = {&a};
   const void* fn = nullptr;
   switch (dtype) {

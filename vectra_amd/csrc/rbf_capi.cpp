@@ -91,6 +91,11 @@ int validate(const vectra_rbf_args* a) {
     return VECTRA_ERR_BAD_SHAPE;
   if (a->variant < VECTRA_VARIANT_AUTO || a->variant > VECTRA_VARIANT_TILE)
     return VECTRA_ERR_BAD_VARIANT;
+  // Each size below 2^31 keeps every product of two or three of them in int64.
+  constexpr int64_t kMaxDim = 0x7fffffffLL;
+  if (a->batch > kMaxDim || a->heads > kMaxDim || a->n_q > kMaxDim || a->n_k > kMaxDim ||
+      a->head_dim > kMaxDim || a->value_dim > kMaxDim)
+    return VECTRA_ERR_TOO_LARGE;
   const int64_t rows = a->batch * a->heads * a->n_q;
   if (rows == 0 || a->value_dim == 0) return VECTRA_OK;  // nothing to read or write
   // Buffers with no elements may be NULL (torch gives empty tensors no storage).
@@ -99,6 +104,8 @@ int validate(const vectra_rbf_args* a) {
     return VECTRA_ERR_NULL_ARGUMENT;
   // Kernels index query rows with 32-bit wave ids.
   if (rows > 0x7fffffffLL) return VECTRA_ERR_TOO_LARGE;
+  // The generic kernel's grid has one row of workgroups per 256 value columns.
+  if ((a->value_dim + 255) / 256 > vectra::kMaxGenericSlices) return VECTRA_ERR_TOO_LARGE;
   return VECTRA_OK;
 }
 
@@ -241,10 +248,11 @@ int vectra_rbf_squared_norms(const void* x, int32_t dtype, int64_t batch, int64_
                              vectra_stream_t stream) {
   if (!is_io_dtype(dtype)) return VECTRA_ERR_BAD_DTYPE;
   if (batch < 0 || heads < 0 || rows < 0 || cols < 0) return VECTRA_ERR_BAD_SHAPE;
-  const int64_t n = batch * heads * rows;
-  if (n == 0) return VECTRA_OK;
+  if (batch == 0 || heads == 0 || rows == 0) return VECTRA_OK;
   if (x == nullptr || out == nullptr || x_stride == nullptr) return VECTRA_ERR_NULL_ARGUMENT;
-  if ((n + 255) / 256 > 0x7fffffffLL) return VECTRA_ERR_TOO_LARGE;
+  // The kernel loops over rows with a grid stride, so any row count fits its
+  // grid; rows are 64-bit.  B*H*N must not overflow int64.
+  if (rows > INT64_MAX / batch / heads) return VECTRA_ERR_TOO_LARGE;
   const hipError_t err = vectra::launch_squared_norms(x, dtype, batch, heads, rows, cols, x_stride,
                                                       out, reinterpret_cast<hipStream_t>(stream));
   return err == hipSuccess ? VECTRA_OK : VECTRA_ERR_LAUNCH;

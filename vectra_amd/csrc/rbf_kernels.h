@@ -16,7 +16,9 @@ void make_fast_div(int64_t d, uint32_t* mul, uint32_t* shift);
 // chunks in {2, 4, 8, 16}.
 hipError_t launch_stream(Problem& p, int in_dtype, int out_dtype, int chunks, hipStream_t s);
 
-// Generic kernel: any strides and sizes.
+// Generic kernel: any strides and sizes.  Its grid has one row of
+// workgroups per 256-column slice of Dv, at most this many.
+constexpr int64_t kMaxGenericSlices = 65535;
 hipError_t launch_generic(Problem& p, int in_dtype, int out_dtype, hipStream_t s);
 
 // MFMA kernel: bf16/fp16/fp32 inputs, output in the input dtype or fp32,

@@ -42,8 +42,12 @@ bool plane_supports(const Problem& p, int in_dtype, int out_dtype) {
   if (kRows * p.sq[2] * esize > kMax32 || kRows * p.sk[2] * esize > kMax32 || kRows * p.sv[2] * esize > kMax32)
     return false;
   if (p.bias != nullptr && kRows * p.sbn * (p.bias_dtype == VECTRA_F32 ? 4 : 2) > kMax32) return false;
-  // Output offsets inside a plane are 32-bit element counts.
-  if (p.so[2] < 0 || p.so[3] < 0 || (p.Nq - 1) * p.so[2] + (p.Dv - 1) * p.so[3] > 0x7fffffffLL) return false;
+  // Output offsets inside a plane are 32-bit byte counts: the last element of
+  // the plane's output view must lie within 4 GiB of the plane's first.
+  const int64_t out_size = out_dtype == VECTRA_F32 ? 4 : 2;
+  if (p.so[2] < 0 || p.so[3] < 0 ||
+      ((p.Nq - 1) * p.so[2] + (p.Dv - 1) * p.so[3]) * out_size + out_size - 1 > kMax32)
+    return false;
   // Plane indices (and plane + grid size) are 32-bit.
   return p.B * p.H < (int64_t{1} << 30);
 }

@@ -24,8 +24,9 @@
 //  * key blocks past Nk are skipped, and up to 4 keys past the last whole
 //    block (65 keys: one) go through the VALU instead of a block of products
 //    that would be mostly padding.
-// Weights are used unshifted while a query's sum stays in [2^-100, 2^100]
-// (no fp32 overflow, and subnormal weights under 2^-20 of the sum); outside
+// Weights are used unshifted while a query's sum stays in [2^-100, 2^32]
+// (value products overflow only for |v| > 2^96, and subnormal weights lie
+// under 2^-20 of the sum); outside
 // that range (gamma < 0, a query far from every key, biases far from 0) the
 // wave's blocks are computed once more with each query's exact maximum
 // subtracted.  The distance is not clamped at zero, as in the 16-bit kernel.
@@ -64,7 +65,11 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
   constexpr int kPer = 2;  // query blocks per wave
   constexpr int kChunks = G::kChunks;
   constexpr int kSteps = G::kSteps;
-  constexpr float kSumHi = 0x1p100f;
+  // Weights are used unshifted while a query's sum stays in [2^-100, 2^32]:
+  // then |acc| <= 2^32 * max|v|, so the value products cannot overflow
+  // unless |v| exceeds 2^96.  Outside the range the block is recomputed with
+  // each query's maximum subtracted.
+  constexpr float kSumHi = 0x1p32f;
   constexpr float kSumLo = 0x1p-100f;
   // K pieces and V pieces a lane loads before the first wait: all of them
   // when the workgroup has at least kPieces / 256 waves (three for 65 queries

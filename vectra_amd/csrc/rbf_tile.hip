@@ -26,8 +26,12 @@ bool tile_supports(const Problem& p, int in_dtype, int out_dtype) {
       ((p.Nk - 1) * p.sv[2] + p.Dv) * 2 > kMax32)
     return false;
   if (p.bias != nullptr && (p.Nk - 1) * p.sbn * (p.bias_dtype == VECTRA_F32 ? 4 : 2) + 4 > kMax32) return false;
-  // Output offsets inside a plane are 32-bit element counts.
-  if (p.so[2] < 0 || p.so[3] < 0 || (p.Nq - 1) * p.so[2] + (p.Dv - 1) * p.so[3] > 0x7fffffffLL) return false;
+  // Output offsets inside a plane are 32-bit byte counts: the last element of
+  // the plane's output view must lie within 4 GiB of the plane's first.
+  const int64_t out_size = out_dtype == VECTRA_F32 ? 4 : 2;
+  if (p.so[2] < 0 || p.so[3] < 0 ||
+      ((p.Nq - 1) * p.so[2] + (p.Dv - 1) * p.so[3]) * out_size + out_size - 1 > kMax32)
+    return false;
   // Work items (planes x blocks of 128 query rows) and item + grid size are 32-bit.
   return p.B * p.H * ((p.Nq + 127) / 128) < (int64_t{1} << 30);
 }

@@ -1,6 +1,6 @@
 """torch.ops.vectra.rbf_attention on MI355X.
 
-Same operator as the reference's kernels/vectra_kernels/custom_ops.py:62-115:
+Same operator as the reference's kernels/vectra_kernels/custom_ops.py:52-97 (op :52-72, 'cuda' kernel :75-85, fake :88-97):
 
   out = torch.ops.vectra.rbf_attention(q, k, v, scale, key_bias=None)
 
@@ -32,7 +32,7 @@ def hip_available() -> bool:
 
 @torch.library.register_fake(OP_NAME)
 def _rbf_attention_fake(q, k, v, scale, key_bias=None):
-    """Shape and dtype only (custom_ops.py:106-115): (*q.shape[:-1], Dv), v.dtype."""
+    """Shape and dtype only (custom_ops.py:88-97): (*q.shape[:-1], Dv), v.dtype."""
     del k, scale, key_bias  # Only the output shape matters while tracing.
     return q.new_empty((*q.shape[:-1], v.shape[-1]), dtype=v.dtype)
 
