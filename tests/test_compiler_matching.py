@@ -1,18 +1,35 @@
-"""What the `vectra` pass must and must not rewrite (CPU Inductor).
+"""Which code the `vectra` pass rewrites, and which it must leave alone
+(CPU Inductor).
 
-Restates the reference's compiler/tests/test_pattern_matching.py:33-246:
-idiomatic spellings of RBF attention are found and rewritten; look-alikes
-that compute something else are left alone and keep their eager results.
+Behaviour restated from the reference's compiler/tests/test_pattern_matching.py:
+any idiomatic spelling of RBF attention becomes one vectra::rbf_attention
+site with unchanged results; code that computes something else, however
+close in form, keeps its eager graph and its eager results.  Here the
+spellings are composed from interchangeable parts (a squared distance, a
+logit, a normaliser) and each look-alike changes one part of a correct
+spelling.
 """
+
+import itertools
 
 import pytest
 import torch
 from torch import fx
 
-from tests.compiler_helpers import attention_inputs, compile_and_run
+from tests import compiler_helpers as ch
 from vectra_amd.compiler import pattern
 
-F = torch.nn.functional
+TOL = {'rtol': 1e-4, 'atol': 1e-5}
+
+DISTANCES = (ch.distance_broadcast_pow, ch.distance_indexed_self_product, ch.distance_functional_square)
+LOGITS = (ch.logit_over_two_sigma_squared, ch.logit_times_negative_reciprocal, ch.logit_negated_product,
+          ch.logit_fixed_temperature)
+NORMALISERS = (ch.normalise_softmax, ch.normalise_functional, ch.normalise_exp_over_sum)
+
+# Every distance with every logit under softmax, and every normaliser with
+# the model's own distance and logit.
+SPELLINGS = [ch.spelling(d, lg, ch.normalise_softmax) for d, lg in itertools.product(DISTANCES, LOGITS)]
+SPELLINGS += [ch.spelling(ch.distance_broadcast_pow, ch.logit_over_two_sigma_squared, n) for n in NORMALISERS[1:]]
 
 
 @pytest.fixture(autouse=True)
@@ -22,179 +39,127 @@ def _fresh_dynamo():
     torch._dynamo.reset()  # pylint: disable=protected-access
 
 
-# --- Spellings that must be rewritten. --------------------------------------
-
-
-def method_chain(q, k, v, sigma):
-    sq_dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-1)
-    return torch.softmax(-sq_dist / (2 * sigma**2), dim=-1) @ v
-
-
-def functional_calls(q, k, v, sigma):
-    diff = torch.sub(torch.unsqueeze(q, 3), torch.unsqueeze(k, 2))
-    sq_dist = torch.sum(torch.square(diff), dim=-1)
-    gamma = torch.reciprocal(2.0 * sigma * sigma)
-    return torch.matmul(F.softmax(torch.mul(sq_dist, -gamma), dim=-1), v)
-
-
-def indexing_and_products(q, k, v, sigma):
-    diff = q[:, :, :, None, :] - k[:, :, None, :, :]
-    sq_dist = (diff * diff).sum(dim=4)
-    weights = torch.exp(-(sq_dist * (0.5 / sigma**2)))
-    return weights / weights.sum(dim=-1, keepdim=True) @ v
-
-
-def literal_temperature(q, k, v, sigma):
-    del sigma
-    sq_dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-1)
-    return torch.softmax(sq_dist * -0.125, dim=-1) @ v
-
-
-class MaskedHead(torch.nn.Module):
-    def forward(self, q, k, v, sigma, valid):
-        bias = torch.zeros_like(valid, dtype=q.dtype).masked_fill(~valid, float('-inf'))[:, None, None, :]
-        sq_dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-1)
-        return torch.softmax(-sq_dist / (2 * sigma.pow(2)) + bias, -1) @ v
-
-
-@pytest.mark.parametrize(
-    'fn', [method_chain, functional_calls, indexing_and_products, literal_temperature],
-    ids=lambda fn: fn.__name__,
-)
-def test_spellings_are_rewritten(fn):
-    q, k, v, sigma = attention_inputs()
-    out, report = compile_and_run(fn, q, k, v, sigma)
+@pytest.mark.parametrize('fn', SPELLINGS, ids=lambda fn: fn.__name__)
+def test_each_spelling_becomes_one_site(fn):
+    ops = ch.operands(seed=7)
+    out, report = ch.run_vectra(fn, *ops)
     assert report.sites == 1, report.matches
-    torch.testing.assert_close(out, fn(q, k, v, sigma), rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(out, fn(*ops), **TOL)
 
 
-def test_masked_attention_is_rewritten_with_its_bias():
-    q, k, v, sigma = attention_inputs(n_k=10)
-    valid = torch.ones(2, 10, dtype=torch.bool)
-    valid[0, 7:] = False
-    module = MaskedHead()
-    out, report = compile_and_run(module, q, k, v, sigma, valid)
+def test_a_padding_mask_is_carried_as_the_key_bias():
+    class Padded(torch.nn.Module):
+        def forward(self, q, k, v, sigma, keep):
+            bias = torch.where(keep, 0.0, float('-inf')).to(q.dtype).unsqueeze(1).unsqueeze(1)
+            sq = ch.distance_broadcast_pow(q, k)
+            return torch.softmax(-sq / (2 * sigma.pow(2)) + bias, -1) @ v
+
+    ops = ch.operands(n_k=11, seed=3)
+    keep = torch.ones(2, 11, dtype=torch.bool)
+    keep[1, 6:] = False
+    out, report = ch.run_vectra(Padded(), *ops, keep)
     assert report.matches == {'rbf_divisor_bias_softmax[fp32]': 1}
-    torch.testing.assert_close(out, module(q, k, v, sigma, valid), rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(out, Padded()(*ops, keep), **TOL)
 
 
-def test_every_site_in_a_graph_is_rewritten():
-    q, k, v, sigma = attention_inputs(n_q=9, n_k=9)
+def test_stacked_sites_are_all_rewritten():
+    first = ch.spelling(ch.distance_broadcast_pow, ch.logit_over_two_sigma_squared, ch.normalise_softmax)
+    second = ch.spelling(ch.distance_indexed_self_product, ch.logit_negated_product, ch.normalise_exp_over_sum)
 
-    def two_layers(q, k, v, sigma):
-        h = method_chain(q, k, v, sigma)
-        return indexing_and_products(h, k, v, sigma) + h
+    def stack(q, k, v, sigma):
+        hidden = first(q, k, v, sigma)  # feeds the second site's queries
+        return second(hidden, k, v, sigma) - 0.5 * hidden
 
-    out, report = compile_and_run(two_layers, q, k, v, sigma)
-    assert report.sites == 2
-    torch.testing.assert_close(out, two_layers(q, k, v, sigma), rtol=1e-4, atol=1e-5)
+    ops = ch.operands(n_q=5, n_k=5, seed=11)
+    out, report = ch.run_vectra(stack, *ops)
+    assert report.sites == 2, report.matches
+    torch.testing.assert_close(out, stack(*ops), **TOL)
 
 
-def test_value_layout_does_not_matter():
-    q, k, v, sigma = attention_inputs(n_k=8, dim=8)
-    v_t = v.transpose(-1, -2).contiguous().transpose(-1, -2)
-    out, report = compile_and_run(method_chain, q, k, v_t, sigma)
+def test_a_column_major_value_tensor_is_matched():
+    fn = SPELLINGS[0]
+    ops = ch.operands(n_k=8, dim=8, seed=5)
+    v_cols = ops.v.mT.contiguous().mT  # same values, transposed strides
+    assert not v_cols.is_contiguous()
+    out, report = ch.run_vectra(fn, ops.q, ops.k, v_cols, ops.sigma)
     assert report.sites == 1
-    torch.testing.assert_close(out, method_chain(q, k, v, sigma), rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(out, fn(*ops), **TOL)
 
 
-# --- Look-alikes that must not be rewritten. --------------------------------
+# --------------------------------------------------------- look-alikes
+#
+# Each changes one aspect of a correct spelling.  They run at Nq == Nk == D
+# so that every one of them is well-formed.
+
+def _softmax_over(logits, v):
+    return torch.softmax(logits, dim=-1) @ v
 
 
-def l1_distance(q, k, v, sigma):
-    dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).abs().sum(-1)
-    return torch.softmax(-dist / (2 * sigma**2), dim=-1) @ v
+LOOKALIKES = {
+    'l1_distance': lambda q, k, v, s: _softmax_over(-(q.unsqueeze(-2) - k.unsqueeze(-3)).abs().sum(-1) / (2 * s**2),
+                                                      v),
+    'cubed_gap': lambda q, k, v, s: _softmax_over(-(q.unsqueeze(-2) - k.unsqueeze(-3)).pow(3).sum(-1) / (2 * s**2),
+                                                    v),
+    'summed_over_keys': lambda q, k, v, s: _softmax_over(
+        -(q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-2) / (2 * s**2), v),
+    'normalised_over_queries': lambda q, k, v, s: torch.softmax(
+        -ch.distance_broadcast_pow(q, k) / (2 * s**2), dim=-2) @ v,
+    'positive_exponent': lambda q, k, v, s: _softmax_over(ch.distance_broadcast_pow(q, k) / (2 * s**2), v),
+    'log_weights': lambda q, k, v, s: torch.log_softmax(-ch.distance_broadcast_pow(q, k) / (2 * s**2), -1) @ v,
+    'dot_product_scores': lambda q, k, v, s: _softmax_over(q @ k.mT / s, v),
+    'one_scale_per_key': lambda q, k, v, s: _softmax_over(
+        -ch.distance_broadcast_pow(q, k) * torch.linspace(0.1, 1.0, k.shape[-2], dtype=q.dtype), v),
+    'one_bias_per_query': lambda q, k, v, s: _softmax_over(
+        -ch.distance_broadcast_pow(q, k) / (2 * s**2) + 0.1 * torch.arange(q.shape[-2], dtype=q.dtype)[:, None], v),
+    'no_value_product': lambda q, k, v, s: torch.softmax(-ch.distance_broadcast_pow(q, k) / (2 * s**2), dim=-1),
+}
 
 
-def cubed_difference(q, k, v, sigma):
-    dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(3).sum(-1)
-    return torch.softmax(-dist / (2 * sigma**2), dim=-1) @ v
-
-
-def reduced_over_keys(q, k, v, sigma):
-    dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-2)
-    return torch.softmax(-dist / (2 * sigma**2), dim=-1) @ v
-
-
-def normalized_over_queries(q, k, v, sigma):
-    sq_dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-1)
-    return torch.softmax(-sq_dist / (2 * sigma**2), dim=-2) @ v
-
-
-def no_negation(q, k, v, sigma):
-    sq_dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-1)
-    return torch.softmax(sq_dist / (2 * sigma**2), dim=-1) @ v
-
-
-def log_softmax_weights(q, k, v, sigma):
-    sq_dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-1)
-    return torch.log_softmax(-sq_dist / (2 * sigma**2), dim=-1) @ v
-
-
-def dot_product_attention(q, k, v, sigma):
-    return torch.softmax(q @ k.transpose(-1, -2) / sigma, dim=-1) @ v
-
-
-def per_key_scale(q, k, v, sigma):
-    del sigma
-    sq_dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-1)
-    scale = torch.linspace(0.1, 1.0, k.shape[-2], dtype=q.dtype)
-    return torch.softmax(-sq_dist * scale, dim=-1) @ v
-
-
-def per_query_bias(q, k, v, sigma):
-    sq_dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-1)
-    bias = torch.arange(q.shape[-2], dtype=q.dtype)[:, None] * 0.1
-    return torch.softmax(-sq_dist / (2 * sigma**2) + bias, dim=-1) @ v
-
-
-def weights_only(q, k, v, sigma):
-    del v
-    sq_dist = (q.unsqueeze(-2) - k.unsqueeze(-3)).pow(2).sum(-1)
-    return torch.softmax(-sq_dist / (2 * sigma**2), dim=-1)
-
-
-@pytest.mark.parametrize(
-    'fn',
-    [l1_distance, cubed_difference, reduced_over_keys, normalized_over_queries, no_negation,
-     log_softmax_weights, dot_product_attention, per_key_scale, per_query_bias, weights_only],
-    ids=lambda fn: fn.__name__,
-)
-def test_lookalikes_are_not_rewritten(fn):
-    q, k, v, sigma = attention_inputs(n_q=8, n_k=8, dim=8)  # Nq == Nk == D
-    out, report = compile_and_run(fn, q, k, v, sigma)
+@pytest.mark.parametrize('name', sorted(LOOKALIKES))
+def test_lookalikes_keep_their_eager_graph(name):
+    fn = LOOKALIKES[name]
+    ops = ch.operands(n_q=8, n_k=8, dim=8, seed=13)
+    out, report = ch.run_vectra(fn, *ops)
     assert report.sites == 0, report.matches
-    torch.testing.assert_close(out, fn(q, k, v, sigma), rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(out, fn(*ops), **TOL)
 
 
-# --- The catalog. -----------------------------------------------------------
+# ------------------------------------------------------------ catalog
+
+def test_the_catalog_holds_every_formulation_in_every_precision():
+    entries = pattern.load_catalog('cpu')
+    assert len(pattern.CATALOG) == 8  # coefficient x bias x normalisation
+    assert {e.spec for e in entries} == set(pattern.CATALOG)
+    names = [e.name for e in entries]
+    assert len(names) == len(set(names))
+    by_precision = {}
+    for e in entries:
+        by_precision.setdefault(e.precision, []).append(e)
+    # softmax upcasts half inputs, so it has per-precision templates; exp over
+    # sum traces alike in every dtype, so one template serves all of them.
+    softmax = {e.precision for e in entries if e.spec.normalization == 'softmax'}
+    exp_sum = {e.precision for e in entries if e.spec.normalization != 'softmax'}
+    assert softmax <= {'fp32', 'half', 'autocast'} and exp_sum <= {'any', 'autocast'}
+    assert sum(len(v) for k, v in by_precision.items() if k != 'autocast') == 12
 
 
-def test_catalog_covers_every_formulation_and_precision():
-    catalog = pattern.load_catalog('cpu')
-    assert {e.spec for e in catalog} == set(pattern.CATALOG)
-    assert len(pattern.CATALOG) == 8
-    assert len({e.name for e in catalog}) == len(catalog)
-    for e in catalog:
-        # torch.softmax upcasts half precision; exp / sum decomposes alike.
-        if e.spec.normalization == 'softmax':
-            assert e.precision in ('fp32', 'half', 'autocast')
-        else:
-            assert e.precision in ('any', 'autocast')
-    reference_style = [e for e in catalog if e.precision != 'autocast']
-    assert len(reference_style) == 12
-    for e in catalog:
-        names = [n.name for n in e.graph_module.graph.nodes if n.op == 'placeholder']
-        assert len(names) == len(e.spec.placeholder_names)
-        assert names[-1] == pattern.V_BMM
-        targets = {n.target for n in e.graph_module.graph.nodes}
-        assert torch.ops.aten.bmm.default in targets
-        assert torch.ops.aten.pow.Tensor_Scalar in targets
+@pytest.mark.parametrize('entry', pattern.load_catalog('cpu'), ids=lambda e: e.name)
+def test_templates_bind_their_value_cut_last(entry):
+    graph = entry.graph_module.graph
+    inputs = [n.name for n in graph.find_nodes(op='placeholder')]
+    assert len(inputs) == len(entry.spec.placeholder_names)
+    assert inputs[-1] == pattern.V_BMM
+    used = {n.target for n in graph.nodes if n.op == 'call_function'}
+    assert {torch.ops.aten.bmm.default, torch.ops.aten.pow.Tensor_Scalar} <= used
 
 
-def test_squares_are_canonicalized():
+def test_a_product_of_a_node_with_itself_becomes_a_square():
     graph = fx.Graph()
     x = graph.placeholder('x')
-    graph.output(graph.call_function(torch.ops.aten.mul.Tensor, (x, x)))
+    y = graph.placeholder('y')
+    graph.output((graph.call_function(torch.ops.aten.mul.Tensor, (x, x)),
+                  graph.call_function(torch.ops.aten.mul.Tensor, (x, y))))
     assert pattern.canonicalize_squares(graph) == 1
-    assert [n.target for n in graph.nodes if n.op == 'call_function'] == [torch.ops.aten.pow.Tensor_Scalar]
+    targets = [n.target for n in graph.nodes if n.op == 'call_function']
+    assert sorted(map(str, targets)) == sorted(map(str, [torch.ops.aten.pow.Tensor_Scalar,
+                                                         torch.ops.aten.mul.Tensor]))

@@ -119,7 +119,7 @@ def test_numerics_gate_rejects_a_drifting_model(trained):
     def drifted(*inputs):
         return model(*inputs) + 0.05
 
-    with pytest.raises(compile_entry.NumericsError, match='differs from eager'):
+    with pytest.raises(compile_entry.NumericsError, match='differ from eager'):
         compile_entry.max_abs_error(drifted, model, CONFIG, SPEC, batches=1)
     worst, drift = compile_entry.max_abs_error(model, model, CONFIG, SPEC, batches=2, reference=model)
     assert worst == 0.0 and drift == 0.0

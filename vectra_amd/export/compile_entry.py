@@ -1,17 +1,28 @@
-"""Compiles a checkpoint for serving and writes a release bundle.
+"""Release bundles for the price model: compile, prove, package, reload.
 
   python -m vectra_amd.export.compile_entry --checkpoint-dir ckpt --out bundle \\
       [--device cuda] [--batch-size 1024] [--block-dtype bfloat16]
 
-Restates the reference's models/export/compile_entry.py:145-355 on this
-build: the model is compiled with the `vectra` backend (one graph, every
-attention site rewritten to vectra::rbf_attention, which runs the HIP
-kernels on the GPU), and the compiled model must match the eager model
-(allclose, rtol 1e-3 / atol 1e-3, on seeded serving-shape batches) before the
-bundle is written.  torch.compile is a just-in-time compiler, so a bundle
-holds the verified inputs to compilation -- weights, architecture, serving
-shape and precision, toolchain versions -- with checksums; `load_bundle`
-recompiles at start-up and re-runs the same gates before serving.
+A bundle is a directory holding the checkpoint's two files and a manifest:
+
+  model.safetensors, model_config.json   the checkpoint, copied
+  compile_manifest.json                  what was built and the evidence
+
+torch.compile compiles just in time, so a bundle carries no compiled code.
+It carries the inputs to compilation (weights, architecture, serving shape
+and precision) and a toolchain fingerprint, each file with its SHA-256.  Two
+gates decide whether a compiled model may serve, both when the bundle is
+exported and again when a serving host loads it:
+
+* the compile gate: TorchDynamo captures the model as one graph and the
+  `vectra` backend rewrites one attention site per Transformer block to
+  vectra::rbf_attention (the HIP kernels on the GPU);
+* the numerics gate: on seeded batches of the serving shape, every output of
+  the compiled model lies within |compiled - eager| <= ATOL + RTOL * |eager|
+  of the eager model in the same precision.
+
+Reference behaviour: models/export/compile_entry.py:145-355 (export, gates,
+manifest fields, padded prediction).
 """
 
 import argparse
@@ -20,7 +31,7 @@ import hashlib
 import json
 import os
 import platform
-import shutil
+import tempfile
 import time
 
 import numpy as np
@@ -32,131 +43,188 @@ from vectra_amd.price_transformer import model as model_lib
 
 FORMAT_VERSION = 1
 MANIFEST = 'compile_manifest.json'
-# The numerics gate: compiled must match eager at rtol 1e-3.
 RTOL = 1e-3
 ATOL = 1e-3
 
+# Seeds of the numerics gate's batches: batch i is example_inputs(seed=base + i).
+_GATE_SEED_BASE = 1000
+_BLOCK_DTYPES = {'float32': torch.float32, 'float16': torch.float16, 'bfloat16': torch.bfloat16}
+_COPY_BLOCK = 4 << 20
+
 
 class NumericsError(RuntimeError):
-    """The compiled model disagrees with the eager model."""
+    """The compiled model's outputs leave the numerics gate."""
+
+
+class BundleError(ValueError):
+    """A bundle directory that must not be served as it is."""
 
 
 @dataclasses.dataclass(frozen=True)
 class ServingSpec:
-    """The shape and precision the model is compiled for."""
+    """Where and how the model is compiled: device, static batch, block dtype."""
 
     device: str
     batch_size: int
     block_dtype: str
 
+    def __post_init__(self):
+        if self.block_dtype not in _BLOCK_DTYPES:
+            raise ValueError(f'block_dtype must be one of {sorted(_BLOCK_DTYPES)}, not {self.block_dtype!r}')
+        if self.batch_size < 1:
+            raise ValueError(f'batch_size must be positive, not {self.batch_size}')
+
+    @classmethod
+    def for_device(cls, device: str, batch_size: int, block_dtype: str | None = None) -> 'ServingSpec':
+        return cls(device, batch_size, block_dtype or default_block_dtype(device))
+
     @property
     def dtype(self) -> torch.dtype:
-        return getattr(torch, self.block_dtype)
+        return _BLOCK_DTYPES[self.block_dtype]
 
 
 def default_block_dtype(device: str) -> str:
-    """float16 blocks on the GPU (the reference's default), float32 on CPU."""
+    """Half-precision blocks on a GPU, full precision on the host."""
     return 'float16' if torch.device(device).type == 'cuda' else 'float32'
 
 
 def toolchain_versions() -> dict[str, str]:
-    """Versions that must match between export and serving."""
+    """The fingerprint a serving host must share with the exporting host.
+
+    Inductor generates code for the parts of the model around the attention
+    sites (Triton on the GPU), so its version is part of the fingerprint as
+    well as torch's, HIP's and the C ABI of the attention library.
+    """
     from vectra_amd.kernels import capi  # pylint: disable=import-outside-toplevel
 
-    versions = {
+    try:
+        import triton  # pylint: disable=import-outside-toplevel
+        triton_version = triton.__version__
+    except ImportError:
+        triton_version = 'unavailable'
+    major, minor = capi.abi_version()
+    return {
         'python': platform.python_version(),
         'torch': torch.__version__,
         'numpy': np.__version__,
         'hip': str(torch.version.hip),
-        'vectra_rbf_abi': '%d.%d' % capi.abi_version(),
+        'vectra_rbf_abi': f'{major}.{minor}',
+        'triton': triton_version,
     }
-    try:
-        import triton  # pylint: disable=import-outside-toplevel
-
-        versions['triton'] = triton.__version__
-    except ImportError:
-        versions['triton'] = 'unavailable'
-    return versions
 
 
-def _sha256(path: str) -> str:
+def _file_digest(path: str) -> str:
     digest = hashlib.sha256()
     with open(path, 'rb') as f:
-        for block in iter(lambda: f.read(1 << 22), b''):
-            digest.update(block)
+        while chunk := f.read(_COPY_BLOCK):
+            digest.update(chunk)
     return digest.hexdigest()
 
 
+def _copy_and_digest(src: str, dst: str) -> str:
+    """Copies `src` to `dst` and returns the SHA-256 of the bytes written, in
+    one pass over the data."""
+    digest = hashlib.sha256()
+    with open(src, 'rb') as fin, open(dst, 'wb') as fout:
+        while chunk := fin.read(_COPY_BLOCK):
+            digest.update(chunk)
+            fout.write(chunk)
+    return digest.hexdigest()
+
+
+def _write_json_atomically(path: str, payload: dict) -> None:
+    """The manifest appears complete or not at all: a half-written manifest
+    would otherwise read as a corrupt bundle."""
+    directory = os.path.dirname(os.path.abspath(path))
+    fd, tmp = tempfile.mkstemp(prefix='.manifest-', dir=directory)
+    try:
+        with os.fdopen(fd, 'w', encoding='utf-8') as f:
+            json.dump(payload, f, indent=2, sort_keys=True)
+            f.write('\n')
+        os.replace(tmp, path)
+    except BaseException:
+        if os.path.exists(tmp):
+            os.unlink(tmp)
+        raise
+
+
 def prepare(model: model_lib.PriceTransformer, spec: ServingSpec) -> model_lib.PriceTransformer:
-    """Moves `model` to the serving device and block precision (in place)."""
+    """Puts `model` (in place) on the serving device, in eval mode, with its
+    Transformer blocks in the serving precision."""
     model = model.to(spec.device).eval()
-    if spec.dtype != torch.float32:
+    if spec.dtype is not torch.float32:
         model.set_block_dtype(spec.dtype)
     return model
 
 
+def _largest_gap(a: torch.Tensor, b: torch.Tensor) -> float:
+    return float((a - b).abs().max()) if a.numel() else 0.0
+
+
 def max_abs_error(compiled, eager, config: model_lib.ModelConfig, spec: ServingSpec, batches: int,
                   reference=None) -> tuple[float, float]:
-    """Gates compiled-vs-eager numerics on seeded serving-shape batches.
+    """Runs the numerics gate over `batches` seeded serving-shape batches.
 
-    Returns (worst |compiled - eager|, worst |compiled - reference|), the
-    reference being the fp32 eager model (0.0 without one).  Raises
-    NumericsError when compiled and eager disagree beyond RTOL / ATOL.
+    Returns (largest |compiled - eager|, largest |compiled - reference|); the
+    second is 0.0 without a `reference` (the fp32 eager model, reported but
+    not gated).  Raises NumericsError at the first batch where an output of
+    `compiled` leaves ATOL + RTOL * |eager| (NaN never passes).
     """
-    worst, drift = 0.0, 0.0
+    vs_eager = vs_reference = 0.0
     with torch.no_grad():
-        for seed in range(batches):
-            inputs = model_lib.example_inputs(config, spec.batch_size, spec.device, seed=1000 + seed)
+        for i in range(batches):
+            inputs = model_lib.example_inputs(config, spec.batch_size, spec.device, seed=_GATE_SEED_BASE + i)
             got = compiled(*inputs).float()
             want = eager(*inputs).float()
-            error = (got - want).abs().max().item()
-            if not torch.allclose(got, want, rtol=RTOL, atol=ATOL):
+            gap = _largest_gap(got, want)
+            within = torch.isclose(got, want, rtol=RTOL, atol=ATOL)
+            if not bool(within.all()):
+                bad = int((~within).sum())
                 raise NumericsError(
-                    f'compiled model differs from eager by up to {error:.3g} '
-                    f'(rtol {RTOL}, atol {ATOL}) on seeded batch {seed}'
-                )
-            worst = max(worst, error)
+                    f'gate batch {i}: {bad} of {within.numel()} outputs of the compiled model differ from '
+                    f'eager by more than {ATOL:g} + {RTOL:g}*|eager| (largest gap {gap:.3g})')
+            vs_eager = max(vs_eager, gap)
             if reference is not None:
-                drift = max(drift, (got - reference(*inputs).float()).abs().max().item())
-    return worst, drift
+                vs_reference = max(vs_reference, _largest_gap(got, reference(*inputs).float()))
+    return vs_eager, vs_reference
 
 
 def compile_model(model: model_lib.PriceTransformer, spec: ServingSpec):
-    """(compiled model, CompileReport, compile seconds) for a prepared model."""
-    inputs = model_lib.example_inputs(model.config, spec.batch_size, spec.device)
-    start = time.perf_counter()
-    compiled, report = backend.compile_for_serving(model, tuple(inputs),
-                                                   expected_sites=model.config.num_layers)
-    return compiled, report, time.perf_counter() - start
+    """Compiles a prepared model at the serving shape through the compile
+    gate; returns (compiled model, CompileReport, seconds spent)."""
+    shape_inputs = tuple(model_lib.example_inputs(model.config, spec.batch_size, spec.device))
+    began = time.perf_counter()
+    compiled, report = backend.compile_for_serving(model, shape_inputs, expected_sites=model.config.num_layers)
+    return compiled, report, time.perf_counter() - began
 
 
-def _device_name(device: str) -> str:
+def _device_label(device: str) -> str:
     if torch.device(device).type == 'cuda':
         return torch.cuda.get_device_name(device)
     return platform.processor() or platform.machine()
 
 
 def export_bundle(checkpoint_dir: str, out_dir: str, spec: ServingSpec, numerics_batches: int = 4) -> dict:
-    """Compiles, verifies and writes `out_dir`; returns the manifest."""
+    """Compiles the checkpoint for `spec`, passes both gates, and writes the
+    bundle to `out_dir`.  Returns the manifest that was written."""
     eager = prepare(checkpoint.load(checkpoint_dir), spec)
     compiled, report, seconds = compile_model(eager, spec)
-    reference = checkpoint.load(checkpoint_dir, spec.device) if spec.dtype != torch.float32 else None
-    worst, drift = max_abs_error(compiled, eager, eager.config, spec, numerics_batches, reference)
+    fp32 = checkpoint.load(checkpoint_dir, spec.device) if spec.dtype is not torch.float32 else None
+    vs_eager, vs_fp32 = max_abs_error(compiled, eager, eager.config, spec, numerics_batches, fp32)
+
     os.makedirs(out_dir, exist_ok=True)
-    files = {}
-    for name in (checkpoint.WEIGHTS, checkpoint.CONFIG):
-        shutil.copyfile(os.path.join(checkpoint_dir, name), os.path.join(out_dir, name))
-        files[name] = _sha256(os.path.join(out_dir, name))
+    digests = {name: _copy_and_digest(os.path.join(checkpoint_dir, name), os.path.join(out_dir, name))
+               for name in (checkpoint.WEIGHTS, checkpoint.CONFIG)}
     manifest = {
         'format_version': FORMAT_VERSION,
-        'files': files,
+        'files': digests,
         'model': dataclasses.asdict(eager.config),
-        'serving': dataclasses.asdict(spec) | {'device_name': _device_name(spec.device)},
+        'serving': {**dataclasses.asdict(spec), 'device_name': _device_label(spec.device)},
         'compile': {
             'backend': backend.BACKEND_NAME,
             'expected_sites': eager.config.num_layers,
             'sites': report.sites,
-            'matches': report.matches,
+            'matches': dict(report.matches),
             'graph_count': report.graph_count,
             'graph_break_count': report.graph_break_count,
             'seconds': round(seconds, 3),
@@ -165,23 +233,23 @@ def export_bundle(checkpoint_dir: str, out_dir: str, spec: ServingSpec, numerics
             'rtol': RTOL,
             'atol': ATOL,
             'batches': numerics_batches,
-            'max_abs_error_vs_eager': worst,
-            'max_abs_error_vs_float32_eager': drift,
+            'max_abs_error_vs_eager': vs_eager,
+            'max_abs_error_vs_float32_eager': vs_fp32,
         },
         'versions': toolchain_versions(),
     }
-    with open(os.path.join(out_dir, MANIFEST), 'w', encoding='utf-8') as f:
-        json.dump(manifest, f, indent=2, sort_keys=True)
-        f.write('\n')
+    _write_json_atomically(os.path.join(out_dir, MANIFEST), manifest)
     return manifest
 
 
 class ServingModel:
-    """A compiled model plus the padding that keeps its shape static.
+    """A compiled model behind a request-count-agnostic predict().
 
-    The model is compiled for exactly `batch_size` requests, so a smaller
-    batch is padded with copies of its last request and a larger one is
-    split; padding rows are dropped from the result.
+    The compiled graph takes exactly `spec.batch_size` rows.  predict() walks
+    the requests in windows of that size; each window is gathered with one
+    index_select per input field whose indices run past the last request
+    clamped to it, so a short window is padded with copies of its last
+    request and the padded rows are dropped from the result.
     """
 
     def __init__(self, compiled, config: model_lib.ModelConfig, spec: ServingSpec, manifest: dict):
@@ -191,46 +259,68 @@ class ServingModel:
         self.manifest = manifest
 
     def predict(self, inputs: model_lib.PricingInputs) -> torch.Tensor:
-        """Predicted log prices [n] for a batch of any size n >= 1."""
-        n = inputs.query_embedding.shape[0]
-        b = self.spec.batch_size
-        outputs = []
+        """Log prices [n] for n >= 1 requests, in request order."""
+        n = int(inputs.query_embedding.shape[0])
+        rows = self.spec.batch_size
+        fields = [t.to(self.spec.device) for t in inputs]
+        results = torch.empty(n, dtype=torch.float32, device=self.spec.device)
         with torch.no_grad():
-            for start in range(0, n, b):
-                chunk = [t[start:start + b].to(self.spec.device) for t in inputs]
-                size = chunk[0].shape[0]
-                if size < b:
-                    chunk = [torch.cat([t, t[-1:].expand(b - size, *t.shape[1:])]) for t in chunk]
-                outputs.append(self.compiled(*chunk)[:size].float())
-        return torch.cat(outputs)
+            for first in range(0, n, rows):
+                live = min(rows, n - first)
+                index = torch.arange(first, first + rows, device=self.spec.device).clamp_(max=n - 1)
+                window = [t.index_select(0, index) for t in fields]
+                results[first:first + live] = self.compiled(*window)[:live].float()
+        return results
+
+
+def _read_manifest(bundle_dir: str) -> dict:
+    path = os.path.join(bundle_dir, MANIFEST)
+    try:
+        with open(path, encoding='utf-8') as f:
+            manifest = json.load(f)
+    except (OSError, json.JSONDecodeError) as e:
+        raise BundleError(f'{path} is missing or unreadable: {e}') from e
+    if manifest.get('format_version') != FORMAT_VERSION:
+        raise BundleError(f'{bundle_dir} has bundle format {manifest.get("format_version")!r}; '
+                          f'this build reads format {FORMAT_VERSION}')
+    return manifest
+
+
+def _check_files(bundle_dir: str, manifest: dict) -> None:
+    for name, recorded in sorted(manifest['files'].items()):
+        path = os.path.join(bundle_dir, name)
+        if not os.path.exists(path) or _file_digest(path) != recorded:
+            raise BundleError(f'{name} in {bundle_dir} fails its manifest checksum (SHA-256)')
+
+
+def _check_toolchain(manifest: dict) -> None:
+    here, there = toolchain_versions(), manifest['versions']
+    changed = {k: (there.get(k), here.get(k)) for k in sorted(set(here) | set(there)) if here.get(k) != there.get(k)}
+    if changed:
+        listed = ', '.join(f'{k}: {a} at export, {b} here' for k, (a, b) in changed.items())
+        raise BundleError(f'toolchain differs from the one the bundle was exported with ({listed}); '
+                          're-export the bundle or load it with strict_versions=False')
 
 
 def load_bundle(bundle_dir: str, device: str | None = None, strict_versions: bool = True) -> ServingModel:
-    """Recompiles a bundle and re-verifies it before serving.
+    """Checks a bundle, recompiles it and re-runs both gates before serving.
 
-    `device` overrides the bundle's device (its precision is then that
-    device's default).  Raises ValueError for a corrupt bundle or a toolchain
-    mismatch, NumericsError when the recompiled model disagrees with eager,
-    and the compiler's PatternNotFoundError / GraphBreakError when the
-    rewrite does not apply.
+    `device` moves the bundle to another device, in that device's default
+    block precision.  Raises BundleError (a ValueError) for an unknown format,
+    a file that fails its checksum or, with strict_versions, a different
+    toolchain; NumericsError when the recompiled model leaves the numerics
+    gate; the compiler's PatternNotFoundError / GraphBreakError when the
+    compile gate fails.
     """
-    with open(os.path.join(bundle_dir, MANIFEST), encoding='utf-8') as f:
-        manifest = json.load(f)
-    if manifest.get('format_version') != FORMAT_VERSION:
-        raise ValueError(f'unsupported bundle format in {bundle_dir}')
-    for name, digest in manifest['files'].items():
-        if _sha256(os.path.join(bundle_dir, name)) != digest:
-            raise ValueError(f'{name} does not match its manifest checksum')
-    exported = manifest['versions']
-    if strict_versions and exported != toolchain_versions():
-        raise ValueError(f'toolchain {toolchain_versions()} differs from the export toolchain '
-                         f'{exported}; re-export the bundle')
-    serving = manifest['serving']
-    spec = ServingSpec(
-        device=device or serving['device'],
-        batch_size=serving['batch_size'],
-        block_dtype=serving['block_dtype'] if device is None else default_block_dtype(device),
-    )
+    manifest = _read_manifest(bundle_dir)
+    _check_files(bundle_dir, manifest)
+    if strict_versions:
+        _check_toolchain(manifest)
+    recorded = manifest['serving']
+    if device is None:
+        spec = ServingSpec(recorded['device'], recorded['batch_size'], recorded['block_dtype'])
+    else:
+        spec = ServingSpec.for_device(device, recorded['batch_size'])
     model = prepare(checkpoint.load(bundle_dir), spec)
     compiled, _, _ = compile_model(model, spec)
     max_abs_error(compiled, model, model.config, spec, batches=1)
@@ -238,17 +328,18 @@ def load_bundle(bundle_dir: str, device: str | None = None, strict_versions: boo
 
 
 def main(argv=None) -> None:
-    p = argparse.ArgumentParser(description='Compile and verify a price-model checkpoint for serving.')
-    p.add_argument('--checkpoint-dir', required=True)
-    p.add_argument('--out', required=True)
-    p.add_argument('--device', default='cuda' if torch.cuda.is_available() else 'cpu')
-    p.add_argument('--batch-size', type=int, default=64)
-    p.add_argument('--block-dtype', choices=['float32', 'float16', 'bfloat16'], default=None)
-    p.add_argument('--numerics-batches', type=int, default=4)
-    args = p.parse_args(argv)
-    spec = ServingSpec(args.device, args.batch_size, args.block_dtype or default_block_dtype(args.device))
+    parser = argparse.ArgumentParser(description='Compile a price-model checkpoint, gate it and write a bundle.')
+    parser.add_argument('--checkpoint-dir', required=True, help='directory written by checkpoint.save')
+    parser.add_argument('--out', required=True, help='bundle directory to write')
+    parser.add_argument('--device', default='cuda' if torch.cuda.is_available() else 'cpu')
+    parser.add_argument('--batch-size', type=int, default=64, help='static serving batch')
+    parser.add_argument('--block-dtype', choices=sorted(_BLOCK_DTYPES), default=None,
+                        help='Transformer-block precision (default: float16 on a GPU, float32 on the host)')
+    parser.add_argument('--numerics-batches', type=int, default=4, help='seeded batches the gate compares')
+    args = parser.parse_args(argv)
+    spec = ServingSpec.for_device(args.device, args.batch_size, args.block_dtype)
     manifest = export_bundle(args.checkpoint_dir, args.out, spec, args.numerics_batches)
-    print(json.dumps({'out': args.out, 'compile': manifest['compile'], 'numerics': manifest['numerics']},
+    print(json.dumps({'bundle': args.out, 'compile': manifest['compile'], 'numerics': manifest['numerics']},
                      sort_keys=True))
 
 

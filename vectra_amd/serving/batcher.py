@@ -1,24 +1,33 @@
 """Dynamic batching of concurrent requests into model calls.
 
-`Batcher` has the reference gateway's semantics (serving/predict.py:253-330):
-the first request of a batch opens a window of `window_s`; the batch runs
-when the window closes or `max_batch_size` requests wait, whichever comes
-first; requests that queued behind a running batch join the next one at
-once; the batch function runs on one dedicated thread, so the event loop
-keeps accepting requests; a batch that raises fails only its own requests;
-every result carries its batch size, its queueing time and the batch's
-inference time in microseconds.
+Semantics (the reference gateway's, serving/predict.py:253-330):
 
-On the GPU a batch is two stages: `launch` stages the inputs and enqueues
-the copies and kernels (it returns as soon as the work is queued) and
-`finish` waits for the results.  Given both, the batcher keeps up to `depth`
-batches in flight: it launches the next batch before it waits for the
-previous one, so the host-to-device copy of batch n + 1 overlaps the model's
-work on batch n.  With a single `run_batch` function (depth 1) batches never
-overlap, as in the reference.
+* a batch's window opens when the batcher takes its first request and lasts
+  `window_s`; the batch closes when the window ends or `max_batch_size`
+  requests are waiting, whichever comes first;
+* requests that arrived while the previous batch ran are already waiting, so
+  they join the next batch at once;
+* the model runs off the event loop, so the loop keeps accepting requests;
+* a batch whose function raises fails its own requests only;
+* every result carries its batch size, how long it waited and how long its
+  batch took (microseconds).
+
+Design.  Requests wait in a deque; `submit` appends and sets an
+asyncio.Event.  The collecting coroutine sleeps on that event until the
+window ends or enough requests wait, then takes up to `max_batch_size` from
+the front.
+
+On the GPU a batch is two stages: `launch` stages the inputs and enqueues the
+copies and kernels (it returns once the work is queued) and `finish` waits for
+the results.  Given both, the batcher keeps up to `depth` batches in flight:
+launches run in order on one thread and completions in the same order on
+another, so the next batch's host-to-device copy overlaps the model's work on
+the previous one.  A single `run_batch` function is the depth-1 form, in
+which batches never overlap.
 """
 
 import asyncio
+import collections
 import concurrent.futures
 import dataclasses
 import time
@@ -39,17 +48,27 @@ class Batched(typing.Generic[_Result]):
     inference_us: int
 
 
+@dataclasses.dataclass
+class _Pending:
+    item: typing.Any
+    future: asyncio.Future
+    arrived: float  # perf_counter() at submit
+
+
+def _micros(seconds: float) -> int:
+    return int(seconds * 1e6)
+
+
 class Batcher(typing.Generic[_Item, _Result]):
     """Groups concurrent requests into batched model calls.
 
     Args:
       run_batch: items -> results (one per item, in order); the depth-1 form.
       max_batch_size: largest batch.
-      window_s: how long the first request of a batch waits for others.
+      window_s: how long a batch's first request waits for others.
       launch, finish: the two-stage form instead of `run_batch`:
-        launch(items) -> handle queues the batch's work, finish(handle) ->
-        results waits for it.  Launches run on one thread, in order, and
-        completions on another, in the same order.
+        launch(items) -> handle queues the batch's work and
+        finish(handle) -> results waits for it.
       depth: batches in flight in the two-stage form (>= 1).
     """
 
@@ -65,126 +84,130 @@ class Batcher(typing.Generic[_Item, _Result]):
     ):
         if max_batch_size < 1 or window_s < 0 or depth < 1:
             raise ValueError('need max_batch_size >= 1, window_s >= 0 and depth >= 1')
-        if (run_batch is None) == (launch is None and finish is None):
+        two_stage = launch is not None or finish is not None
+        if (run_batch is not None) == two_stage:
             raise ValueError('give either run_batch or launch and finish')
-        if run_batch is None and (launch is None or finish is None):
+        if two_stage and (launch is None or finish is None):
             raise ValueError('the two-stage form needs both launch and finish')
         if run_batch is not None:
-            launch, finish, depth = (lambda items: run_batch(items)), (lambda results: results), 1
+            launch, finish, depth = run_batch, None, 1
         self._launch = launch
         self._finish = finish
         self._depth = depth
-        self._max_batch_size = max_batch_size
+        self._limit = max_batch_size
         self._window_s = window_s
-        self._queue: asyncio.Queue | None = None
+        self._waiting: collections.deque[_Pending] = collections.deque()
+        self._arrival: asyncio.Event | None = None
         self._task: asyncio.Task | None = None
-        # Launches run on one thread and completions on another, so waiting
-        # for batch n never holds back the launch of batch n + 1.
-        self._launcher = concurrent.futures.ThreadPoolExecutor(max_workers=1, thread_name_prefix='inference')
-        self._finisher = concurrent.futures.ThreadPoolExecutor(max_workers=1, thread_name_prefix='completion')
+        self._launch_thread = concurrent.futures.ThreadPoolExecutor(max_workers=1, thread_name_prefix='inference')
+        self._finish_thread = concurrent.futures.ThreadPoolExecutor(max_workers=1, thread_name_prefix='completion')
+
+    # ------------------------------------------------------------ lifecycle
 
     def start(self) -> None:
-        """Starts the batching loop on the running event loop."""
-        self._queue = asyncio.Queue()
-        self._task = asyncio.get_running_loop().create_task(self._loop())
+        """Starts batching on the running event loop."""
+        self._arrival = asyncio.Event()
+        self._task = asyncio.get_running_loop().create_task(self._serve())
 
     async def close(self) -> None:
-        if self._task is not None:
-            self._task.cancel()
-            try:
-                await self._task
-            except asyncio.CancelledError:
-                pass
-        self._launcher.shutdown(wait=True)
-        self._finisher.shutdown(wait=True)
+        """Stops batching; requests still waiting are cancelled."""
+        task, self._task = self._task, None
+        if task is not None:
+            task.cancel()
+            await asyncio.gather(task, return_exceptions=True)
+        while self._waiting:
+            self._waiting.popleft().future.cancel()
+        self._launch_thread.shutdown(wait=True)
+        self._finish_thread.shutdown(wait=True)
 
     async def submit(self, item: _Item) -> Batched[_Result]:
-        """Queues `item`; resolves when its batch has run.
+        """Queues `item` and returns its result once its batch has run.
 
-        Raises whatever the batch function raised for the item's batch.
+        Raises what the batch function raised for the item's batch.
         """
-        if self._queue is None:
+        if self._arrival is None:
             raise RuntimeError('Batcher.start() was not called')
         future = asyncio.get_running_loop().create_future()
-        await self._queue.put((item, future, time.perf_counter()))
+        self._waiting.append(_Pending(item, future, time.perf_counter()))
+        self._arrival.set()
         return await future
 
-    async def _collect(self) -> list[tuple]:
-        batch = [await self._queue.get()]
-        deadline = time.perf_counter() + self._window_s
-        while len(batch) < self._max_batch_size:
-            try:  # requests that queued behind the previous batch join at once
-                batch.append(self._queue.get_nowait())
-                continue
-            except asyncio.QueueEmpty:
-                pass
-            remaining = deadline - time.perf_counter()
-            if remaining <= 0:
+    # ------------------------------------------------------------ batching
+
+    async def _until_arrival(self, timeout: float | None) -> bool:
+        """Sleeps until a request arrives (True) or `timeout` passes (False)."""
+        self._arrival.clear()
+        try:
+            await asyncio.wait_for(self._arrival.wait(), timeout)
+        except asyncio.TimeoutError:
+            return False
+        return True
+
+    async def _next_batch(self) -> list[_Pending]:
+        while not self._waiting:
+            await self._until_arrival(None)
+        closes = time.perf_counter() + self._window_s
+        while len(self._waiting) < self._limit:
+            left = closes - time.perf_counter()
+            if left <= 0 or not await self._until_arrival(left):
                 break
-            try:
-                batch.append(await asyncio.wait_for(self._queue.get(), remaining))
-            except asyncio.TimeoutError:
-                break
-        return batch
+        taken = [self._waiting.popleft() for _ in range(min(self._limit, len(self._waiting)))]
+        return [p for p in taken if not p.future.cancelled()]
 
     @staticmethod
-    def _fail(batch, error: BaseException) -> None:
-        for _, future, _ in batch:
-            if not future.done():
-                future.set_exception(error)
+    def _reject(batch: list[_Pending], error: BaseException) -> None:
+        for pending in batch:
+            if not pending.future.done():
+                pending.future.set_exception(error)
 
-    async def _complete(self, batch, handle, started: float) -> None:
-        loop = asyncio.get_running_loop()
+    def _results_of(self, handle) -> list:
+        return handle if self._finish is None else self._finish(handle)
+
+    async def _resolve(self, batch: list[_Pending], handle, began: float) -> None:
         try:
-            results = await loop.run_in_executor(self._finisher, self._finish, handle)
+            results = await asyncio.get_running_loop().run_in_executor(self._finish_thread, self._results_of, handle)
             if len(results) != len(batch):
-                raise RuntimeError(f'the batch function returned {len(results)} results '
-                                   f'for {len(batch)} requests')
-        except Exception as e:  # pylint: disable=broad-except
-            # Isolation point: the error belongs to this batch's callers, and
-            # the loop keeps serving later batches.
-            self._fail(batch, e)
+                raise RuntimeError(f'the batch function gave {len(results)} results for {len(batch)} requests')
+        except Exception as error:  # pylint: disable=broad-except
+            # The error belongs to this batch's callers; later batches run on.
+            self._reject(batch, error)
             return
-        inference_us = int((time.perf_counter() - started) * 1e6)
-        for (_, future, queued), result in zip(batch, results):
-            if not future.done():
-                future.set_result(Batched(result, len(batch), int((started - queued) * 1e6), inference_us))
+        took = _micros(time.perf_counter() - began)
+        for pending, value in zip(batch, results):
+            if not pending.future.done():
+                pending.future.set_result(Batched(value, len(batch), _micros(began - pending.arrived), took))
 
-    async def _completer(self, launched: asyncio.Queue, slots: asyncio.Semaphore) -> None:
-        # Batches complete in launch order; each frees its pipeline slot.
+    async def _resolver(self, in_flight: asyncio.Queue, slots: asyncio.Semaphore) -> None:
+        # Batches resolve in launch order, each freeing its slot.
         while True:
-            batch, handle, started = await launched.get()
+            batch, handle, began = await in_flight.get()
             try:
-                await self._complete(batch, handle, started)
+                await self._resolve(batch, handle, began)
             finally:
                 slots.release()
 
-    async def _loop(self) -> None:
+    async def _serve(self) -> None:
         loop = asyncio.get_running_loop()
         slots = asyncio.Semaphore(self._depth)
-        launched: asyncio.Queue = asyncio.Queue()
-        completer = loop.create_task(self._completer(launched, slots))
+        in_flight: asyncio.Queue = asyncio.Queue()
+        resolver = loop.create_task(self._resolver(in_flight, slots))
         try:
             while True:
-                # A slot is free once the batch `depth` places back has
-                # completed; requests queue meanwhile and join the next batch.
+                # The slot of the batch `depth` launches back frees when that
+                # batch resolves; meanwhile requests wait and join the next one.
                 await slots.acquire()
-                batch = await self._collect()
-                batch = [entry for entry in batch if not entry[1].cancelled()]
+                batch = await self._next_batch()
                 if not batch:
                     slots.release()
                     continue
-                started = time.perf_counter()
+                began = time.perf_counter()
                 try:
-                    handle = await loop.run_in_executor(self._launcher, self._launch, [b[0] for b in batch])
-                except Exception as e:  # pylint: disable=broad-except
-                    self._fail(batch, e)
+                    handle = await loop.run_in_executor(self._launch_thread, self._launch, [p.item for p in batch])
+                except Exception as error:  # pylint: disable=broad-except
+                    self._reject(batch, error)
                     slots.release()
                     continue
-                await launched.put((batch, handle, started))
+                await in_flight.put((batch, handle, began))
         finally:
-            completer.cancel()
-            try:
-                await completer
-            except asyncio.CancelledError:
-                pass
+            resolver.cancel()
+            await asyncio.gather(resolver, return_exceptions=True)
