@@ -13,11 +13,21 @@ kernel must match the eager chain (the CPU baseline below) within rtol 1e-3 /
 atol 1e-4 (bf16/fp16 inputs) or 1e-5 / 1e-6 (fp32), and the operator's
 v.dtype output must be exactly that fp32 result rounded once.
 
-The K timed steps are HIP-graph replays of trials of up to 100 operator
-launches (host launch overhead is not the GPU's throughput), bracketed by
-torch.cuda.synchronize() and events on the stream the kernels run on; the
-first trial is queued behind an untimed lead-in replay, so no trial starts
-on an idle GPU (see time_trials).
+A timed step is one launch of the operator's kernel through the C ABI
+(vectra_rbf_attention_fwd, the boundary the operator's GPU implementation
+calls) with the arguments the operator passes for that input set: output in
+v.dtype, automatic kernel selection.  The argument structs are built once,
+so the host enqueues a launch in a few microseconds, well inside a launch's
+GPU time.  The K timed steps run as trials of up to 100 launches, bracketed
+by torch.cuda.synchronize() and by events on the stream the kernels run on;
+the first trial is queued behind an untimed lead-in (one HIP-graph replay
+of launches), so no trial starts on an idle GPU and the host stays ahead of
+the device (see time_trials).  `--launch graph` times HIP-graph replays of
+operator calls instead (each replay adds ~13 us of graph start-up on the GPU
+before its first kernel).
+
+The CPU baseline is timed after the GPU: the GPU then never idles through
+the CPU leg right before its timed region (an idle GPU lowers its clocks).
 
 Prints one JSON line:  queries/s (value), ms_per_step, the roofline of the
 kernel (algorithmic bytes / average launch time vs 8 TB/s) and the CPU
@@ -25,6 +35,7 @@ baseline (the eager chain, torch fp32, on the host cores).
 """
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -67,7 +78,10 @@ def parse_args():
     p.add_argument('--warmup', type=int, default=20)
     p.add_argument('--config', default='serving', choices=sorted(configs.CONFIGS))
     p.add_argument('--dtype', default=None, choices=['bf16', 'fp16', 'fp32'])
-    p.add_argument('--no-graph', action='store_true', help='time a host loop instead of a graph')
+    p.add_argument('--launch', default='capi', choices=['capi', 'graph', 'op'],
+                   help='timed launches: C-ABI calls (default), HIP-graph replays of operator calls, '
+                   'or a host loop of operator calls')
+    p.add_argument('--no-graph', action='store_true', help='same as --launch op')
     p.add_argument('--cpu-seconds', type=float, default=12.0,
                    help='CPU-baseline budget (0 skips the CPU leg; numerics then use the '
                    'bit-exact rounding check only)')
@@ -103,16 +117,26 @@ def cpu_sample(config, inputs):
     return sliced, batches, heads, n_q
 
 
+def cpu_reference(config, host_inputs):
+    """The eager chain (the oracle's restatement of the reference's
+    reference.py:54-58) in torch fp32 on the CPU sample: the numerics gate's
+    comparator.  Returns (output, (batches, heads, query rows) of the sample)."""
+    from oracle import rbf as oracle  # noqa: E402  (cpu_baseline leg only)
+
+    sample, batches, heads, n_q = cpu_sample(config, host_inputs)
+    chunk = 64 if n_q > 1 else None
+    return oracle.eager_fp32(*sample.args(), batch_chunk=chunk), (batches, heads, n_q)
+
+
 def cpu_baseline(config, host_inputs, seconds):
     """Times the eager chain (the oracle's restatement of the reference's
-    reference.py:54-58) in torch fp32 on the host cores; returns (record,
-    sample slice, output on the sample)."""
+    reference.py:54-58) in torch fp32 on the host cores; returns the record."""
     from oracle import rbf as oracle  # noqa: E402  (cpu_baseline leg only)
 
     threads = torch.get_num_threads()
     sample, batches, heads, n_q = cpu_sample(config, host_inputs)
     chunk = 64 if n_q > 1 else None
-    out = oracle.eager_fp32(*sample.args(), batch_chunk=chunk)  # warm-up + reference
+    oracle.eager_fp32(*sample.args(), batch_chunk=chunk)  # warm-up
     reps, start = 0, time.perf_counter()
     while True:
         oracle.eager_fp32(*sample.args(), batch_chunk=chunk)
@@ -158,7 +182,7 @@ def cpu_baseline(config, host_inputs, seconds):
         'op_cpu_path': {'value': op_qps, 'unit': 'queries/s', 'reps': op_reps,
                         'note': 'torch.ops.vectra.rbf_attention on CPU tensors (fused C++ loop), same sample'},
     }
-    return record, (batches, heads, n_q), out
+    return record
 
 
 # The K timed steps run as trials of this many launches (the last trial takes
@@ -166,61 +190,65 @@ def cpu_baseline(config, host_inputs, seconds):
 TRIAL_STEPS = 100
 
 
-# Launches of the lead-in replay that runs, unsynchronised, right before the
-# first timed trial (about 0.8 ms of GPU work at the serving shape).
-LEAD_STEPS = 64
+# The untimed lead-in queued right before the first timed trial (about
+# LEAD_MS of GPU work) and before each later one (about TRIAL_LEAD_MS), each
+# one HIP-graph replay of at most LEAD_MAX_STEPS launches.  The later ones
+# keep the GPU a few milliseconds behind the host even where the host is slow
+# to enqueue (under a profiler's per-launch interception), so the timed
+# launches always run back to back.
+LEAD_MS = 25.0
+TRIAL_LEAD_MS = 12.0
+LEAD_MAX_STEPS = 4096
 
 
-def time_trials(step, steps, warmup, stream, graph=True):
+def time_trials(step, steps, warmup, stream, mode='capi'):
     """Milliseconds per step of each trial of the K = `steps` timed launches.
 
-    Each trial is one HIP-graph replay of its launches (or a host loop with
-    graph=False), bracketed by events on `stream`, the stream the kernels run
-    on; the K launches are bracketed by synchronisations on both sides.
+    `step(i)` enqueues launch i on the current stream.  With mode 'capi' or
+    'op' a trial is a host loop of launches; with 'graph' it is one HIP-graph
+    replay of them (each replay spends ~13 us on the GPU before its first
+    kernel, inside the trial).  Each trial is bracketed by events on
+    `stream`, the stream the kernels run on, and the K launches by
+    synchronisations on both sides.
 
-    With graphs, the W warm-up launches run as one replay, then the device is
-    synchronised, then a lead-in replay of max(W, LEAD_STEPS) launches is
-    queued and the first trial's start event is recorded straight behind it
-    with no synchronisation between.  The host submits the timed replay while
-    the lead-in still runs, so the start event does not fire on an idle GPU
-    and the host's graph-launch latency stays outside the timed region (a
-    trial that starts on an idle GPU times that latency as well).
+    The W warm-up launches run first and the device is synchronised.  Then a
+    lead-in of about LEAD_MS of untimed launches (at least W) is queued as one
+    graph replay and the first trial's start event is recorded straight behind it,
+    with no synchronisation between: the host enqueues the timed launches
+    while the lead-in runs, so the start event does not fire on an idle GPU,
+    the GPU clocks have ramped up, and the host's launch latency stays
+    outside the timed region.  Each later trial is queued behind a shorter
+    lead-in of the same kind (TRIAL_LEAD_MS).
     """
     sizes = [TRIAL_STEPS] * (steps // TRIAL_STEPS) + ([steps % TRIAL_STEPS] if steps % TRIAL_STEPS else [])
-    if graph:
-        side = torch.cuda.Stream()
-        side.wait_stream(stream)
-        with torch.cuda.stream(side):
-            for i in range(3):
+    for i in range(3):  # first launches of each instantiation, outside any capture
+        step(i)
+    torch.cuda.synchronize()
+    probe_start, probe_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    probe_start.record(stream)
+    step(0)
+    probe_end.record(stream)
+    torch.cuda.synchronize()
+    per_launch_ms = max(probe_start.elapsed_time(probe_end), 1e-3)
+    lead_steps = max(warmup, min(LEAD_MAX_STEPS, math.ceil(LEAD_MS / per_launch_ms)))
+    trial_lead_steps = max(1, min(LEAD_MAX_STEPS, math.ceil(TRIAL_LEAD_MS / per_launch_ms)))
+    graphs = {}
+    for size in (set(sizes) if mode == 'graph' else set()) | {lead_steps, trial_lead_steps}:
+        graphs[size] = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graphs[size]):
+            for i in range(size):
                 step(i)
-        stream.wait_stream(side)
-        torch.cuda.synchronize()
-        graphs = {}
-        warm = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(warm):
-            for i in range(max(warmup, 1)):
-                step(i)
-        lead = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(lead):
-            for i in range(max(warmup, LEAD_STEPS)):
-                step(i)
-        for size in set(sizes):
-            graphs[size] = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graphs[size]):
-                for i in range(size):
-                    step(i)
-        warm.replay()
-        torch.cuda.synchronize()
-        lead.replay()  # no synchronisation: the timed replays queue behind it
-    else:
-        for i in range(warmup):
-            step(i)
-        torch.cuda.synchronize()
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    graphs[lead_steps].replay()  # no synchronisation: the trials queue behind it
     events = []
-    for size in sizes:
+    for trial, size in enumerate(sizes):
+        if trial:
+            graphs[trial_lead_steps].replay()  # untimed, unsynchronised
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
-        if graph:
+        if mode == 'graph':
             graphs[size].replay()
         else:
             for i in range(size):
@@ -228,7 +256,7 @@ def time_trials(step, steps, warmup, stream, graph=True):
         end.record(stream)
         events.append((size, start, end))
     torch.cuda.synchronize()
-    return [start.elapsed_time(end) / size for size, start, end in events]
+    return [start.elapsed_time(end) / size for size, start, end in events], lead_steps
 
 
 def load_profile(name):
@@ -267,35 +295,55 @@ def main():
     ]
     torch.cuda.synchronize()
 
-    # ---- CPU baseline leg (also the numerics reference). ----
-    cpu = None
-    if args.cpu_seconds > 0:
-        cpu, (nb, nh, nr), want = cpu_baseline(config, host0, args.cpu_seconds)
-        log(f'cpu baseline: {cpu["value"]:.4g} queries/s on {cpu["cores"]} threads')
-
     # ---- Numerics gate (before any timing). ----
     fp32 = capi.forward(*sets[0].args(), out_dtype=torch.float32)
     out = torch.ops.vectra.rbf_attention(*sets[0].args())
     torch.cuda.synchronize()
     if not torch.equal(out, fp32.to(out.dtype)):
         raise SystemExit('numerics gate: operator output is not the rounded fp32 result')
-    if cpu is not None:
+    if args.cpu_seconds > 0:
+        want, (nb, nh, nr) = cpu_reference(config, host0)
         tol = (1e-5, 1e-6) if config.dtype == torch.float32 else (1e-3, 1e-4)
         torch.testing.assert_close(fp32[:nb, :nh, :nr].cpu(), want, rtol=tol[0], atol=tol[1],
                                    equal_nan=True)
         log('numerics gate passed against the eager chain')
 
-    probe = capi.make_args(*[t for t in (sets[0].q, sets[0].k, sets[0].v)], fp32,
-                           *capi.broadcast_operands(sets[0].q, sets[0].k, sets[0].scale,
-                                                    sets[0].key_bias))
-    variant = capi.VARIANT_NAMES[capi.select_variant(probe)]
-
-    def step(i):
-        return torch.ops.vectra.rbf_attention(*sets[i % n_sets].args())
-
+    # The operator's own launch arguments for each input set: output in
+    # v.dtype (a buffer per set, as the operator allocates one per call),
+    # automatic kernel selection.
+    launches = []
+    for inputs in sets:
+        dst = torch.empty((*inputs.q.shape[:-1], inputs.v.shape[-1]), dtype=inputs.v.dtype, device='cuda')
+        scale4, bias4 = capi.broadcast_operands(inputs.q, inputs.k, inputs.scale, inputs.key_bias)
+        launches.append((capi.make_args(inputs.q, inputs.k, inputs.v, dst, scale4, bias4), dst, scale4, bias4))
+    variant = capi.VARIANT_NAMES[capi.select_variant(launches[0][0])]
     stream = torch.cuda.current_stream()
-    trial_ms = time_trials(step, args.steps, args.warmup, stream, graph=not args.no_graph)
+    mode = 'op' if args.no_graph else args.launch
+    if mode == 'capi':
+        fwd = _native.hip_library().vectra_rbf_attention_fwd
+        arg_refs = [ctypes.byref(entry[0]) for entry in launches]
+
+        def step(i):
+            # The current stream: `stream`, or a capture stream inside a graph capture.
+            status = fwd(arg_refs[i % n_sets], ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if status:
+                raise SystemExit(f'launch failed: {capi.status_string(status)}')
+    else:
+        def step(i):
+            return torch.ops.vectra.rbf_attention(*sets[i % n_sets].args())
+
+    trial_ms, lead_steps = time_trials(step, args.steps, args.warmup, stream, mode=mode)
+    # The timed launches wrote what the operator returns for their sets.
+    for inputs, (_, dst, _, _) in zip(sets, launches):
+        if mode == 'capi' and not torch.equal(dst, torch.ops.vectra.rbf_attention(*inputs.args())):
+            raise SystemExit('the timed launches wrote other values than the operator returns')
     ms = statistics.median(trial_ms)
+
+    # ---- CPU baseline leg, after the GPU timing. ----
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline(config, host0, args.cpu_seconds)
+        log(f'cpu baseline: {cpu["value"]:.4g} queries/s on {cpu["cores"]} threads')
     seconds = ms / 1e3
     fused = roofline.fused_bytes(shape)
     # Bound of the workload: HBM unless its intensity is above the ridge.
@@ -356,8 +404,12 @@ def main():
                         f'Lk={config.n_k} D={config.head_dim}',
             'batch': config.batch, 'heads': config.heads, 'n_q': config.n_q, 'n_k': config.n_k,
             'head_dim': config.head_dim, 'input_sets': n_sets,
-            'timing': ('median over trials of %d launches, each %s' %
-                       (min(TRIAL_STEPS, args.steps), 'a host loop' if args.no_graph else 'one HIP-graph replay')),
+            'timing': ('median over trials of %d launches, each %s, queued behind a graph replay of untimed '
+                       'launches (%d before the first trial, ~12 ms before each later one)' %
+                       (min(TRIAL_STEPS, args.steps),
+                        {'capi': 'a host loop of C-ABI launches with the operator\'s arguments',
+                         'graph': 'one HIP-graph replay of operator calls',
+                         'op': 'a host loop of operator calls'}[mode], lead_steps)),
             'trials': len(trial_ms),
             'variant': variant,
         },

@@ -226,8 +226,10 @@ def test_a_missing_library_fails_loudly(tmp_path):
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     shutil.copytree(os.path.join(root, 'vectra_amd'), tmp_path / 'vectra_amd',
                     ignore=shutil.ignore_patterns('lib', 'csrc', '__pycache__'))
+    env = dict(os.environ, PYTHONPATH=str(tmp_path))
+    env.pop('VECTRA_LIB_DIR', None)  # the copy's own (absent) library directory
     done = subprocess.run([sys.executable, '-c', _MISSING_SCRIPT], cwd=tmp_path, capture_output=True, text=True,
-                          timeout=300, env=dict(os.environ, PYTHONPATH=str(tmp_path)))
+                          timeout=300, env=env)
     assert done.returncode == 0, done.stderr
     lines = done.stdout.strip().splitlines()
     assert len(lines) == 2, lines

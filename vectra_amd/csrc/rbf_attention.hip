@@ -131,6 +131,12 @@ void rbf_stream_kernel(Problem p) {
   constexpr int kPasses = kChunks;  // kPasses * kRowsPerPass == 64 keys
   using Slot = StreamSlot<kPasses>;
 
+  // Every argument read below, loaded in one batch (measured at the serving
+  // shape: 12.4 -> 12.0 us back to back, 12.9 -> 12.65 us per isolated launch).
+  args_in_sgprs(p.q, p.k, p.v, p.out, p.scale, p.bias, p.scale_dtype, p.bias_dtype, p.H, p.Nq, p.Nk);
+  args_in_sgprs(p.sq[0], p.sq[1], p.sq[2], p.sk[0], p.sk[1], p.sk[2], p.sv[0], p.sv[1], p.sv[2]);
+  args_in_sgprs(p.so[0], p.so[1], p.so[2], p.ssb, p.ssh, p.sbb, p.sbh, p.sbn, p.total_rows);
+  args_in_sgprs(p.grid_waves, p.nq_mul, p.nq_shift, p.h_mul, p.h_shift);
   const int lane = threadIdx.x & (kWave - 1);
   const int32_t wave_id =
       static_cast<int32_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

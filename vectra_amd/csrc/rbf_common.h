@@ -34,6 +34,20 @@ struct Problem {
   uint32_t h_mul, h_shift;    // FastDiv of H
 };
 
+// Loads the given kernel arguments into scalar registers at this point: the
+// compiler then issues all of their scalar loads as one batch with one wait.
+// Left to itself it loads each argument where it is first used, which in a
+// prologue with branches becomes several dependent rounds of scalar-cache
+// latency before a wave can issue its first vector load.
+template <typename T>
+__device__ __forceinline__ void arg_in_sgprs(const T& a) {
+  asm volatile("" ::"s"(a));
+}
+template <typename... A>
+__device__ __forceinline__ void args_in_sgprs(const A&... a) {
+  (arg_in_sgprs(a), ...);
+}
+
 // floor(n / d) for 0 <= n < 2^31 from a multiplier and shift made on the host
 // (make_fast_div): mul == 0 means d is a power of two, else
 // mul = ceil(2^(31+l) / d) with l = ceil(log2 d) and shift = l - 1.  Then

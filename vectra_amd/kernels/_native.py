@@ -6,6 +6,9 @@
 
 Both are produced by ``make -C vectra_amd/csrc`` (``__graft_entry__.build()``).
 There is no fallback: if they are missing, importing the operator fails.
+
+``VECTRA_LIB_DIR`` names another directory holding both libraries; the
+host-sanitizer build (``make -C vectra_amd/csrc sanitize-test``) uses it.
 """
 
 import ctypes
@@ -14,7 +17,8 @@ import os
 
 import torch
 
-LIB_DIR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), 'lib')
+LIB_DIR = os.environ.get('VECTRA_LIB_DIR') or os.path.join(
+    os.path.dirname(os.path.dirname(os.path.abspath(__file__))), 'lib')
 HIP_LIBRARY = os.path.join(LIB_DIR, 'libvectra_rbf.so')
 TORCH_LIBRARY = os.path.join(LIB_DIR, 'libvectra_torch.so')
 
