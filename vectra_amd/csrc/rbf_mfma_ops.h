@@ -33,8 +33,25 @@ struct MfmaOps<__bf16> {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
   }
   // Two weights as packed bf16 hi (round to nearest, v_cvt_pk_bf16_f32) and
-  // lo = bf16(w - hi): hi + lo = w to ~2^-17.
+  // lo = bf16(w - hi): hi + lo = w to ~2^-17.  w - hi is exact in fp32 and
+  // comes from one v_dot2 per weight (hi . (-1, 0) + w), which reads the
+  // packed hi directly.  The (-1, 0) and (0, -1) pairs are passed in
+  // registers: as an inline constant, the compiler encodes bf16 pair
+  // (-1, 0) as the 32-bit constant -1.0, which the hardware reads as (0, -1).
   static __device__ __forceinline__ void split2(float w0, float w1, uint32_t& hi, uint32_t& lo) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{w0, w1}, b2));
+    const b2 h = __builtin_bit_cast(b2, hi);
+    uint32_t neg_lo = 0x0000bf80u, neg_hi = 0xbf800000u;  // bf16 pairs (-1, 0), (0, -1)
+    asm("" : "+v"(neg_lo), "+v"(neg_hi));
+    const float d0 = __builtin_amdgcn_fdot2_f32_bf16(h, __builtin_bit_cast(b2, neg_lo), w0, false);
+    const float d1 = __builtin_amdgcn_fdot2_f32_bf16(h, __builtin_bit_cast(b2, neg_hi), w1, false);
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{d0, d1}, b2));
+  }
+  // The same split with hi widened by shifts and w - hi by subtractions: two
+  // more instructions per pair, but no registers for the (-1, 0) pairs (for
+  // kernels at their register limit).
+  static __device__ __forceinline__ void split2_sub(float w0, float w1, uint32_t& hi, uint32_t& lo) {
     typedef __bf16 b2 __attribute__((ext_vector_type(2)));
     hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{w0, w1}, b2));
     const float h0 = __uint_as_float(hi << 16), h1 = __uint_as_float(hi & 0xffff0000u);
@@ -55,14 +72,35 @@ struct MfmaOps<_Float16> {
   }
   // Two weights as packed fp16 hi (round toward zero, v_cvt_pkrtz_f16_f32)
   // and lo = fp16(w - hi), w - hi being exact in fp32: hi + lo = w to ~2^-20.
+  // w - hi comes from one v_dot2 per weight, as for bf16 (fp16 denormals are
+  // kept: the kernels run in the default IEEE mode).
   static __device__ __forceinline__ void split2(float w0, float w1, uint32_t& hi, uint32_t& lo) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     const h2 h = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(w0, w1));
     hi = __builtin_bit_cast(uint32_t, h);
-    lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(w0 - static_cast<float>(h[0]),
-                                                                 w1 - static_cast<float>(h[1])));
+    const float d0 = __builtin_amdgcn_fdot2(h, h2{static_cast<_Float16>(-1.f), static_cast<_Float16>(0.f)}, w0, false);
+    const float d1 = __builtin_amdgcn_fdot2(h, h2{static_cast<_Float16>(0.f), static_cast<_Float16>(-1.f)}, w1, false);
+    lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(d0, d1));
+  }
+  static __device__ __forceinline__ void split2_sub(float w0, float w1, uint32_t& hi, uint32_t& lo) {
+    split2(w0, w1, hi, lo);  // the fp16 constants are inline: no registers
   }
 };
+
+// gfx950's transposing LDS read (ds_read_b64_tr_b16) of 16-bit elements.
+// Within each group of 16 lanes, lane i receives element i % 4 of the 8-byte
+// pieces addressed by lanes i / 4, 4 + i / 4, 8 + i / 4 and 12 + i / 4: with
+// lane i addressing row r0 + i / 4, elements 4 (i % 4) .. +3 of row-major
+// data, lane i gets element i of rows r0 .. r0 + 3 (the A operand of a
+// 16-deep product read from a row-major B).  The mapping was checked on the
+// device.
+typedef short lds_v4s __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const void* p) {
+  // A C-style cast converts the generic pointer to the LDS address space.
+  const lds_v4s r =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) lds_v4s*)(const_cast<void*>(p)));
+  return __builtin_bit_cast(uint2, r);
+}
 
 // Two fp32 values as one 32-bit word of two OutT (round to nearest even,
 // each value first materialised in fp32: see from_float).

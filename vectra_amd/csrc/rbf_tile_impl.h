@@ -89,16 +89,6 @@ struct TileStage {
   uint32_t bias_misalign;
 };
 
-// The 4 16-bit elements ds_read_b64_tr_b16 returns (see the A operand of
-// O^T in rbf_tile_kernel).
-typedef short tile_v4s __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint2 lds_read_tr16(const void* p) {
-  // A C-style cast converts the generic pointer to the LDS address space.
-  const tile_v4s r =
-      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) tile_v4s*)(const_cast<void*>(p)));
-  return __builtin_bit_cast(uint2, r);
-}
-
 // Pass kinds of one item.
 enum TilePass : int { kPassSum = 0, kPassMax = 1, kPassShifted = 2 };
 
@@ -284,8 +274,8 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
           float w[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) w[r] = __builtin_amdgcn_exp2f(x[cb][hb][r] - shift);
-          Ops::split2(w[0], w[1], hi[2 * hb], lo[2 * hb]);
-          Ops::split2(w[2], w[3], hi[2 * hb + 1], lo[2 * hb + 1]);
+          Ops::split2_sub(w[0], w[1], hi[2 * hb], lo[2 * hb]);
+          Ops::split2_sub(w[2], w[3], hi[2 * hb + 1], lo[2 * hb + 1]);
         }
         p_hi[cb] = __builtin_bit_cast(Qk, make_uint4(hi[0], hi[1], hi[2], hi[3]));
         p_lo[cb] = __builtin_bit_cast(Qk, make_uint4(lo[0], lo[1], lo[2], lo[3]));
