@@ -1,0 +1,198 @@
+"""The HIP distance scans (libvectra_scan.so) against the reference's own
+outputs and the CPU restatement, bit for bit (GPU).
+
+Every comparison is on the float32 bit patterns: the kernels keep the
+reference's order of operations (engine/src/index/simd_distance.cc), so any
+difference is a bug, not rounding.  NaN outputs (invalid candidate ids, NaN
+inputs) are compared as NaN.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import scan as oracle
+from vectra_amd.index import scan
+from vectra_amd.kernels import _native
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden', 'scan_golden.npz')
+
+
+def _same(got, want, msg=''):
+    got = np.asarray(got.cpu() if isinstance(got, torch.Tensor) else got, dtype=np.float32)
+    want = np.asarray(want, dtype=np.float32)
+    assert got.shape == want.shape, (got.shape, want.shape, msg)
+    both_nan = np.isnan(got) & np.isnan(want)
+    g = np.where(both_nan, 0, got.view(np.uint32))
+    w = np.where(both_nan, 0, want.view(np.uint32))
+    bad = np.flatnonzero(g != w)
+    assert bad.size == 0, f'{msg}: {bad.size} differ, first at {bad[:5]}: {got.ravel()[bad[:5]]} vs {want.ravel()[bad[:5]]}'
+
+
+def _gpu(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.fixture(scope='module')
+def golden():
+    with np.load(GOLDEN) as data:
+        return dict(data)
+
+
+def test_the_scan_library_is_the_one_loaded():
+    _native.scan_library()
+    assert _native.SCAN_LIBRARY in _native.loaded_libraries()
+
+
+def test_row_distances_equal_the_reference_outputs(golden):
+    for key in [k for k in golden if k.startswith('rows_')]:
+        dim = key.split('_')[1]
+        rows, query = _gpu(golden[key]), _gpu(golden[f'query_{dim}'][None])
+        print(f'rows dim {dim}', flush=True)
+        _same(scan.l2_squared_distances(query, rows)[0], golden[f'l2_{dim}'], f'l2 dim {dim}')
+        _same(scan.inner_products(query, rows)[0], golden[f'ip_{dim}'], f'ip dim {dim}')
+        _same(scan.squared_norms(rows), golden[f'norm_{dim}'], f'norm dim {dim}')
+
+
+def test_adc_and_tables_equal_the_reference_outputs(golden):
+    for key in [k for k in golden if k.startswith('adc_codes_')]:
+        m = key.rsplit('_', 1)[1]
+        got = scan.pq_adc_distances(_gpu(golden[f'adc_table_{m}'][None]), _gpu(golden[key]))
+        _same(got[0], golden[f'adc_{m}'], f'adc m {m}')
+    for key in [k for k in golden if k.startswith('books_')]:
+        _, dim, m = key.split('_')
+        got = scan.pq_distance_tables(_gpu(golden[f'tquery_{dim}_{m}'][None]), _gpu(golden[key]), int(m))
+        _same(got[0], golden[f'table_{dim}_{m}'], key)
+
+
+@pytest.mark.parametrize('dim', [1, 5, 16, 17, 64, 100, 128, 129, 257, 1000])
+@pytest.mark.parametrize('queries', [1, 3, 4, 9])
+def test_row_scans_against_the_oracle(dim, queries):
+    rng = np.random.default_rng(dim * 31 + queries)
+    n = 3001
+    rows = (rng.standard_normal((n, dim)) * np.exp2(rng.integers(-8, 9, size=(n, 1)))).astype(np.float32)
+    q = rng.standard_normal((queries, dim)).astype(np.float32)
+    print(f'dim {dim} queries {queries}', flush=True)
+    _same(scan.l2_squared_distances(_gpu(q), _gpu(rows)), oracle.distances(q, rows, 'l2'), 'l2')
+    _same(scan.inner_products(_gpu(q), _gpu(rows)), oracle.distances(q, rows, 'ip'), 'ip')
+    _same(scan.squared_norms(_gpu(rows)), oracle.squared_norms(rows), 'norm')
+
+
+def test_strided_rows_and_queries_and_candidate_ids():
+    rng = np.random.default_rng(5)
+    dim, n = 77, 2000
+    wide = torch.from_numpy(rng.standard_normal((n, 96)).astype(np.float32)).cuda()
+    rows = wide[:, 3:3 + dim]                  # row stride 96, offset 3 elements
+    qwide = torch.from_numpy(rng.standard_normal((6, 130)).astype(np.float32)).cuda()
+    queries = qwide[:, 10:10 + dim]
+    ids_np = rng.integers(0, n, 700).astype(np.int32)
+    ids_np[[0, 5, 9]] = [n, n + 1000, 2**31 - 1]  # past the rows: NaN, and nothing read
+    ids_np[10:20] = ids_np[20]                  # repeats
+    ids = torch.from_numpy(ids_np).cuda()
+    want_ids = ids_np.astype(np.int64)
+    valid = want_ids < n
+    rows_np, q_np = rows.cpu().numpy(), queries.cpu().numpy()
+    want = np.full((6, 700), np.nan, np.float32)
+    want[:, valid] = oracle.distances(q_np, rows_np, 'l2', want_ids[valid])
+    got = scan.l2_squared_distances(queries, rows, ids=ids)
+    _same(got, want, 'strided l2 with ids')
+    assert torch.isnan(got[:, [0, 5, 9]]).all()
+    # uint32 ids and a caller-provided output
+    out = torch.full((6, 700), 7.0, device='cuda')
+    scan.inner_products(queries, rows, ids=ids.view(torch.uint32), out=out)
+    want_ip = np.full((6, 700), np.nan, np.float32)
+    want_ip[:, valid] = oracle.distances(q_np, rows_np, 'ip', want_ids[valid])
+    _same(out, want_ip, 'strided ip with uint32 ids')
+
+
+def test_special_values_propagate_like_the_reference():
+    dim = 40
+    rows = np.ones((6, dim), np.float32)
+    rows[1, 3] = np.inf
+    rows[2, 20] = np.nan
+    rows[3, 39] = -np.inf                       # in the tail
+    rows[4, :] = 3e19                           # squares overflow to inf
+    rows[5, :] = 1e-23                          # products underflow to subnormals and zero
+    q = np.zeros((1, dim), np.float32)
+    q[0, 3] = np.inf                            # inf - inf = NaN in row 1
+    for fn, metric in ((scan.l2_squared_distances, 'l2'), (scan.inner_products, 'ip')):
+        _same(fn(_gpu(q), _gpu(rows)), oracle.distances(q, rows, metric), metric)
+    _same(scan.squared_norms(_gpu(rows)), oracle.squared_norms(rows), 'norm')
+
+
+def test_a_full_shard_scan_equals_the_oracle():
+    # One query against 2^20 rows of 128 floats (a quarter of a shard at the
+    # reference's max_elements; configs/hnsw_params.textproto).
+    rng = np.random.default_rng(11)
+    n, dim = 1 << 20, 128
+    rows = rng.standard_normal((n, dim), dtype=np.float32)
+    q = rng.standard_normal((1, dim), dtype=np.float32)
+    got = scan.l2_squared_distances(_gpu(q), _gpu(rows))
+    _same(got[0], oracle.l2_squared(q[0], rows), 'shard scan')
+
+
+@pytest.mark.parametrize('m', [1, 2, 3, 4, 5, 7, 8, 16, 17, 31, 32, 64, 65, 100, 256])
+def test_adc_scans_against_the_oracle(m):
+    rng = np.random.default_rng(m)
+    n, queries = 4099, 3
+    tables = (rng.standard_normal((queries, m * 256)) * 20).astype(np.float32)
+    codes = rng.integers(0, 256, (n, m), dtype=np.uint8)
+    got = scan.pq_adc_distances(_gpu(tables), _gpu(codes))
+    want = np.stack([oracle.pq_adc(tables[i], codes) for i in range(queries)])
+    print(f'adc m {m}', flush=True)
+    _same(got, want, f'adc m {m}')
+
+
+def test_adc_with_unaligned_codes_and_ids():
+    rng = np.random.default_rng(2)
+    n, m = 3000, 16
+    wide = torch.from_numpy(rng.integers(0, 256, (n, 19), dtype=np.uint8)).cuda()
+    codes = wide[:, 1:1 + m]                   # stride 19 bytes, base offset 1: byte loads
+    tables = (rng.standard_normal((2, m * 256)) * 5).astype(np.float32)
+    ids_np = rng.integers(0, n, 500).astype(np.int32)
+    ids_np[7] = n                               # past the codes: NaN
+    got = scan.pq_adc_distances(_gpu(tables), codes, ids=torch.from_numpy(ids_np).cuda())
+    codes_np = codes.cpu().numpy()
+    want = np.full((2, 500), np.nan, np.float32)
+    ok = ids_np < n
+    for i in range(2):
+        want[i, ok] = oracle.pq_adc(tables[i], codes_np[ids_np[ok]])
+    _same(got, want, 'unaligned adc with ids')
+
+
+@pytest.mark.parametrize('dim,m', [(128, 16), (128, 8), (96, 32), (256, 8), (48, 3), (512, 16), (17, 17), (272, 8)])
+def test_tables_against_the_oracle(dim, m):
+    rng = np.random.default_rng(dim + m)
+    books = rng.standard_normal((m, 256, dim // m)).astype(np.float32)
+    queries = rng.standard_normal((5, dim)).astype(np.float32)
+    got = scan.pq_distance_tables(_gpu(queries), _gpu(books), m)
+    want = np.stack([oracle.pq_distance_table(queries[i], books, m) for i in range(5)])
+    _same(got, want, f'tables dim {dim} m {m}')
+
+
+def test_tables_then_adc_rank_like_the_reference_search():
+    # ComputeDistanceTable then PqAdcDistance over every code, as
+    # engine/tests/tools/index_study.cc:79-83 does per query.
+    rng = np.random.default_rng(9)
+    dim, m, n = 128, 16, 20000
+    books = rng.standard_normal((m, 256, dim // m)).astype(np.float32)
+    queries = rng.standard_normal((4, dim)).astype(np.float32)
+    codes = rng.integers(0, 256, (n, m), dtype=np.uint8)
+    tables = scan.pq_distance_tables(_gpu(queries), _gpu(books), m)
+    got = scan.pq_adc_distances(tables, _gpu(codes))
+    want = np.stack([oracle.pq_adc(oracle.pq_distance_table(queries[i], books, m), codes) for i in range(4)])
+    _same(got, want, 'tables + adc')
+
+
+def test_empty_inputs():
+    rows = torch.zeros(0, 16, device='cuda')
+    assert scan.l2_squared_distances(torch.zeros(2, 16, device='cuda'), rows).shape == (2, 0)
+    assert scan.squared_norms(rows).shape == (0,)
+    assert scan.pq_adc_distances(torch.zeros(1, 256, device='cuda'),
+                                 torch.zeros(0, 1, dtype=torch.uint8, device='cuda')).shape == (1, 0)
+    zero_dim = scan.l2_squared_distances(torch.zeros(1, 0, device='cuda'), torch.zeros(5, 0, device='cuda'))
+    assert zero_dim.tolist() == [[0.0] * 5]

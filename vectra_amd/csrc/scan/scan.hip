@@ -1,0 +1,400 @@
+// Distance scans of the engine's vector search on gfx950: the C ABI of
+// include/vectra_scan.h and its kernels (libvectra_scan.so).
+//
+// Every output equals, bit for bit, what the reference function returns for
+// the same inputs (engine/src/index/simd_distance.cc, pq_codec.cc), because
+// each kernel performs the reference's floating-point operations in the
+// reference's order:
+//
+// * Row distances (L2SquaredDistance :36-51, InnerProduct :53-62,
+//   SquaredNorm :64-66).  The reference keeps sixteen accumulators: element
+//   i + j of every full 16-element step is added to accumulator j, then the
+//   accumulators are folded pairwise (ReduceLanes :27-32, widths 8, 4, 2, 1)
+//   and the last dimension % 16 elements are added one at a time.  Here the
+//   sixteen accumulators are sixteen lanes: a group of 16 lanes computes one
+//   distance, lane j loading element i + j of each step (one 64-byte segment
+//   per row and step, so a wave reads four rows' segments per load), the fold
+//   is a shuffle tree over the group with the same pairs, and the tail terms,
+//   computed in parallel by lanes 0 .. tail - 1, are added in order.  A group
+//   keeps up to four queries' accumulators, so a row is read once for four
+//   queries.
+// * ADC distances (PqAdcDistance :68-81): one lane per code, four chains over
+//   sub-spaces s .. s + 3, combined as (l0 + l1) + (l2 + l3), then the
+//   remaining sub-spaces; the query's table sits in LDS when it fits.
+// * ADC tables (ProductQuantizer::ComputeDistanceTable, pq_codec.cc:208-217):
+//   one lane per (query, sub-space, centroid), the L2 reduction above written
+//   out sequentially in one lane.
+//
+// No multiply is fused into an add (this file is compiled with
+// -ffp-contract=off, and the pragma below says the same), matching the
+// reference's ISO C++ build.  The scans are bound by HBM reads of the rows or
+// codes; nothing here is reshaped into a matrix product, which would change
+// the order of the sums.
+#pragma clang fp contract(off)
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "vectra_scan.h"
+
+namespace vectra_scan {
+namespace {
+
+constexpr int kLanes = 16;                       // accumulators of one distance
+constexpr int kThreads = 256;                    // per workgroup
+constexpr int kGroupsPerBlock = kThreads / kLanes;
+constexpr int kUnroll = 8;                       // 16-element steps loaded together
+constexpr int kQueryBlock = 4;                   // queries sharing one read of a row
+constexpr int64_t kMaxBlocksX = 1 << 20;         // grid-stride beyond this
+constexpr int64_t kMaxBlocksY = 65535;
+constexpr int kMaxLdsTableSubspaces = 64;        // 64 KiB of LDS per table
+
+struct RowScan {
+  const float* queries;
+  const float* rows;
+  const uint32_t* ids;
+  float* out;
+  int64_t query_stride, row_stride, out_stride;
+  int64_t num_rows, num_cand;
+  int32_t dim, num_queries;
+};
+
+// The term one element adds to an accumulator.
+template <int kMetric>
+__device__ __forceinline__ float term(float query, float row) {
+  if constexpr (kMetric == VECTRA_SCAN_L2_SQUARED) {
+    const float d = query - row;
+    return d * d;
+  } else {
+    return query * row;  // inner product; the squared norm passes the row twice
+  }
+}
+
+template <int kMetric, int kQB>
+__global__ __launch_bounds__(kThreads) void scan_rows_kernel(RowScan p) {
+  constexpr bool kNorm = kMetric == VECTRA_SCAN_SQUARED_NORM;
+  const int lane = static_cast<int>(threadIdx.x) & (kLanes - 1);
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) / kLanes;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kGroupsPerBlock;
+  const int q0 = static_cast<int>(blockIdx.y) * kQB;
+  const int nq = min(kQB, p.num_queries - q0);  // >= 1: the grid has no empty query blocks
+  const int full = p.dim - p.dim % kLanes;
+  const int tail = p.dim - full;
+  // Lane `lane`'s element of query q0 + j is at qlane + j * query_stride.
+  const float* qlane = kNorm ? nullptr : p.queries + static_cast<int64_t>(q0) * p.query_stride + lane;
+
+  for (int64_t cand = first; cand < p.num_cand; cand += step) {
+    int64_t row = cand;
+    bool valid = true;
+    if (p.ids != nullptr) {
+      const uint32_t id = p.ids[cand];
+      valid = static_cast<int64_t>(id) < p.num_rows;
+      row = id;
+    }
+    const float* rlane = p.rows + (valid ? row : 0) * p.row_stride + lane;
+    float acc[kQB];
+#pragma unroll
+    for (int j = 0; j < kQB; ++j) acc[j] = 0.f;
+    if (valid) {
+      int i = 0;
+      for (; i + kLanes * kUnroll <= full; i += kLanes * kUnroll) {
+        float rv[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) rv[u] = rlane[i + kLanes * u];
+#pragma unroll
+        for (int j = 0; j < kQB; ++j) {
+          if (j < nq) {
+            float qv[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u)
+              qv[u] = kNorm ? rv[u] : qlane[static_cast<int64_t>(j) * p.query_stride + i + kLanes * u];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) acc[j] = acc[j] + term<kMetric>(qv[u], rv[u]);
+          }
+        }
+      }
+      for (; i < full; i += kLanes) {
+        const float r = rlane[i];
+#pragma unroll
+        for (int j = 0; j < kQB; ++j) {
+          if (j < nq) {
+            const float q = kNorm ? r : qlane[static_cast<int64_t>(j) * p.query_stride + i];
+            acc[j] = acc[j] + term<kMetric>(q, r);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kQB; ++j) {
+      if (j >= nq) break;
+      // ReduceLanes: lane i < width adds lane i + width, widths 8, 4, 2, 1.
+      float sum = acc[j];
+#pragma unroll
+      for (int width = kLanes / 2; width > 0; width /= 2) {
+        const float other = __shfl_down(sum, width, kLanes);
+        if (lane < width) sum = sum + other;
+      }
+      // The tail, element by element in order (lane k holds element full + k).
+      float t = 0.f;
+      if (valid && lane < tail) {
+        const float r = rlane[full];
+        t = term<kMetric>(kNorm ? r : qlane[static_cast<int64_t>(j) * p.query_stride + full], r);
+      }
+      for (int k = 0; k < tail; ++k) sum = sum + __shfl(t, k, kLanes);
+      if (lane == 0) p.out[static_cast<int64_t>(q0 + j) * p.out_stride + cand] = valid ? sum : NAN;
+    }
+  }
+}
+
+struct PqTable {
+  const float* queries;
+  const float* codebooks;
+  float* tables;
+  int64_t query_stride, table_stride, total;  // total = num_queries * subspaces * 256
+  int32_t subspaces, dsub;
+};
+
+// One lane per table entry: L2SquaredDistance(sub-vector, centroid, dsub)
+// with the reference's sixteen accumulators held in registers.
+__global__ __launch_bounds__(kThreads) void pq_table_kernel(PqTable p) {
+  // total < 2^31 (checked on the host): 32-bit index arithmetic.
+  for (uint32_t t = blockIdx.x * kThreads + threadIdx.x; t < static_cast<uint32_t>(p.total); t += gridDim.x * kThreads) {
+    const int c = static_cast<int>(t % VECTRA_PQ_CENTROIDS);
+    const uint32_t qs = t / VECTRA_PQ_CENTROIDS;
+    const int s = static_cast<int>(qs % static_cast<uint32_t>(p.subspaces));
+    const int64_t q = qs / static_cast<uint32_t>(p.subspaces);
+    const float* sub = p.queries + q * p.query_stride + static_cast<int64_t>(s) * p.dsub;
+    const float* centroid = p.codebooks + (static_cast<int64_t>(s) * VECTRA_PQ_CENTROIDS + c) * p.dsub;
+    float lanes[kLanes];
+#pragma unroll
+    for (int j = 0; j < kLanes; ++j) lanes[j] = 0.f;
+    const int full = p.dsub - p.dsub % kLanes;
+    for (int i = 0; i < full; i += kLanes) {
+#pragma unroll
+      for (int j = 0; j < kLanes; ++j) lanes[j] = lanes[j] + term<VECTRA_SCAN_L2_SQUARED>(sub[i + j], centroid[i + j]);
+    }
+#pragma unroll
+    for (int width = kLanes / 2; width > 0; width /= 2) {
+#pragma unroll
+      for (int j = 0; j < width; ++j) lanes[j] = lanes[j] + lanes[j + width];
+    }
+    float sum = lanes[0];
+    for (int i = full; i < p.dsub; ++i) sum = sum + term<VECTRA_SCAN_L2_SQUARED>(sub[i], centroid[i]);
+    p.tables[q * p.table_stride + static_cast<int64_t>(s) * VECTRA_PQ_CENTROIDS + c] = sum;
+  }
+}
+
+struct PqAdc {
+  const float* tables;
+  const uint8_t* codes;
+  const uint32_t* ids;
+  float* out;
+  int64_t table_stride, code_stride, out_stride;
+  int64_t num_codes, num_cand;
+  int32_t subspaces;
+  int32_t words;  // codes may be read as 32-bit words (4-byte aligned base and stride)
+};
+
+// PqAdcDistance for one code; `entry(s, c)` reads table[s * 256 + c].
+template <typename Entry>
+__device__ __forceinline__ float adc_sum(const uint8_t* code, int m, bool words, Entry entry) {
+  float l0 = 0.f, l1 = 0.f, l2 = 0.f, l3 = 0.f;
+  int s = 0;
+  if (words) {
+    for (; s + 4 <= m; s += 4) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(code + s);
+      l0 = l0 + entry(s, w & 0xffu);
+      l1 = l1 + entry(s + 1, (w >> 8) & 0xffu);
+      l2 = l2 + entry(s + 2, (w >> 16) & 0xffu);
+      l3 = l3 + entry(s + 3, w >> 24);
+    }
+  } else {
+    for (; s + 4 <= m; s += 4) {
+      l0 = l0 + entry(s, code[s]);
+      l1 = l1 + entry(s + 1, code[s + 1]);
+      l2 = l2 + entry(s + 2, code[s + 2]);
+      l3 = l3 + entry(s + 3, code[s + 3]);
+    }
+  }
+  float sum = (l0 + l1) + (l2 + l3);
+  for (; s < m; ++s) sum = sum + entry(s, code[s]);
+  return sum;
+}
+
+template <bool kLdsTable>
+__global__ __launch_bounds__(kThreads) void pq_adc_kernel(PqAdc p) {
+  extern __shared__ float table_lds[];  // subspaces * 256 floats when kLdsTable
+  const int64_t q = blockIdx.y;
+  const float* table = p.tables + q * p.table_stride;
+  const int m = p.subspaces;
+  if constexpr (kLdsTable) {
+    for (int i = static_cast<int>(threadIdx.x); i < m * VECTRA_PQ_CENTROIDS; i += kThreads) table_lds[i] = table[i];
+    __syncthreads();
+  }
+  for (int64_t cand = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; cand < p.num_cand;
+       cand += static_cast<int64_t>(gridDim.x) * kThreads) {
+    int64_t index = cand;
+    bool valid = true;
+    if (p.ids != nullptr) {
+      const uint32_t id = p.ids[cand];
+      valid = static_cast<int64_t>(id) < p.num_codes;
+      index = id;
+    }
+    float sum = NAN;
+    if (valid) {
+      const uint8_t* code = p.codes + index * p.code_stride;
+      if constexpr (kLdsTable) {
+        sum = adc_sum(code, m, p.words != 0,
+                      [&](int s, uint32_t c) { return table_lds[s * VECTRA_PQ_CENTROIDS + static_cast<int>(c)]; });
+      } else {
+        sum = adc_sum(code, m, p.words != 0,
+                      [&](int s, uint32_t c) { return table[s * VECTRA_PQ_CENTROIDS + static_cast<int>(c)]; });
+      }
+    }
+    p.out[q * p.out_stride + cand] = sum;
+  }
+}
+
+unsigned blocks_for(int64_t items, int per_block) {
+  int64_t blocks = (items + per_block - 1) / per_block;
+  if (blocks > kMaxBlocksX) blocks = kMaxBlocksX;
+  return static_cast<unsigned>(blocks < 1 ? 1 : blocks);
+}
+
+int launched(hipError_t e) { return e == hipSuccess ? VECTRA_SCAN_OK : VECTRA_SCAN_LAUNCH_FAILED; }
+
+template <int kMetric>
+int launch_rows(const RowScan& p, hipStream_t stream) {
+  void* args[] = {const_cast<RowScan*>(&p)};
+  const unsigned bx = blocks_for(p.num_cand, kGroupsPerBlock);
+  if (p.num_queries == 1 || kMetric == VECTRA_SCAN_SQUARED_NORM) {
+    return launched(hipLaunchKernel(reinterpret_cast<const void*>(&scan_rows_kernel<kMetric, 1>), dim3(bx, 1),
+                                    dim3(kThreads), args, 0, stream));
+  }
+  const unsigned by = static_cast<unsigned>((p.num_queries + kQueryBlock - 1) / kQueryBlock);
+  return launched(hipLaunchKernel(reinterpret_cast<const void*>(&scan_rows_kernel<kMetric, kQueryBlock>),
+                                  dim3(bx, by), dim3(kThreads), args, 0, stream));
+}
+
+}  // namespace
+}  // namespace vectra_scan
+
+using namespace vectra_scan;
+
+extern "C" int vectra_scan_rows(const vectra_scan_args* a, hipStream_t stream) {
+  if (a == nullptr) return VECTRA_SCAN_INVALID_ARGUMENT;
+  const bool norm = a->metric == VECTRA_SCAN_SQUARED_NORM;
+  if (a->metric < VECTRA_SCAN_L2_SQUARED || a->metric > VECTRA_SCAN_SQUARED_NORM) return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (a->dimension < 0 || a->num_queries < 0 || a->num_rows < 0 || (a->ids != nullptr && a->num_ids < 0))
+    return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (norm && a->num_queries != 1) return VECTRA_SCAN_INVALID_ARGUMENT;
+  const int64_t cand = a->ids != nullptr ? a->num_ids : a->num_rows;
+  if (a->row_stride < a->dimension || a->out_stride < cand) return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (!norm && a->query_stride < a->dimension) return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (a->num_queries == 0 || cand == 0) return VECTRA_SCAN_OK;
+  // Vectors of zero floats are never read (their distances are 0).
+  const bool reads = a->dimension > 0;
+  if (a->out == nullptr || (reads && a->num_rows > 0 && a->rows == nullptr) || (reads && !norm && a->queries == nullptr))
+    return VECTRA_SCAN_INVALID_ARGUMENT;
+  if ((a->num_queries + kQueryBlock - 1) / kQueryBlock > kMaxBlocksY) return VECTRA_SCAN_TOO_LARGE;
+  // Element offsets stay below 2^62.
+  const int64_t lim = int64_t{1} << 62;
+  if ((a->num_rows > 0 && a->row_stride > lim / a->num_rows) || a->out_stride > lim / a->num_queries ||
+      (!norm && a->query_stride > lim / a->num_queries))
+    return VECTRA_SCAN_TOO_LARGE;
+  RowScan p;
+  p.queries = a->queries;
+  p.rows = a->rows;
+  p.ids = a->ids;
+  p.out = a->out;
+  p.query_stride = a->query_stride;
+  p.row_stride = a->row_stride;
+  p.out_stride = a->out_stride;
+  p.num_rows = a->num_rows;
+  p.num_cand = cand;
+  p.dim = a->dimension;
+  p.num_queries = static_cast<int32_t>(a->num_queries);
+  switch (a->metric) {
+    case VECTRA_SCAN_L2_SQUARED: return launch_rows<VECTRA_SCAN_L2_SQUARED>(p, stream);
+    case VECTRA_SCAN_INNER_PRODUCT: return launch_rows<VECTRA_SCAN_INNER_PRODUCT>(p, stream);
+    default: return launch_rows<VECTRA_SCAN_SQUARED_NORM>(p, stream);
+  }
+}
+
+extern "C" int vectra_pq_distance_tables(const vectra_pq_table_args* a, hipStream_t stream) {
+  if (a == nullptr) return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (a->subspaces <= 0 || a->dimension <= 0 || a->dimension % a->subspaces != 0 || a->num_queries < 0)
+    return VECTRA_SCAN_INVALID_ARGUMENT;
+  const int64_t entries = static_cast<int64_t>(a->subspaces) * VECTRA_PQ_CENTROIDS;
+  if (a->query_stride < a->dimension || a->table_stride < entries) return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (a->num_queries == 0) return VECTRA_SCAN_OK;
+  if (a->queries == nullptr || a->codebooks == nullptr || a->tables == nullptr) return VECTRA_SCAN_INVALID_ARGUMENT;
+  const int64_t lim = int64_t{1} << 62;
+  if (a->table_stride > lim / a->num_queries || a->query_stride > lim / a->num_queries) return VECTRA_SCAN_TOO_LARGE;
+  if (a->num_queries > (int64_t{1} << 31) / entries - 1) return VECTRA_SCAN_TOO_LARGE;  // entries in total < 2^31
+  PqTable p;
+  p.queries = a->queries;
+  p.codebooks = a->codebooks;
+  p.tables = a->tables;
+  p.query_stride = a->query_stride;
+  p.table_stride = a->table_stride;
+  p.total = a->num_queries * entries;
+  p.subspaces = a->subspaces;
+  p.dsub = a->dimension / a->subspaces;
+  void* args[] = {&p};
+  return launched(hipLaunchKernel(reinterpret_cast<const void*>(&pq_table_kernel), dim3(blocks_for(p.total, kThreads)),
+                                  dim3(kThreads), args, 0, stream));
+}
+
+extern "C" int vectra_scan_pq_adc(const vectra_pq_adc_args* a, hipStream_t stream) {
+  if (a == nullptr) return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (a->subspaces < 1 || a->subspaces > VECTRA_PQ_CENTROIDS || a->num_queries < 0 || a->num_codes < 0 ||
+      (a->ids != nullptr && a->num_ids < 0))
+    return VECTRA_SCAN_INVALID_ARGUMENT;
+  const int64_t cand = a->ids != nullptr ? a->num_ids : a->num_codes;
+  const int64_t entries = static_cast<int64_t>(a->subspaces) * VECTRA_PQ_CENTROIDS;
+  if (a->table_stride < entries || a->code_stride < a->subspaces || a->out_stride < cand)
+    return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (a->num_queries == 0 || cand == 0) return VECTRA_SCAN_OK;
+  if (a->tables == nullptr || a->out == nullptr || (a->num_codes > 0 && a->codes == nullptr))
+    return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (a->num_queries > kMaxBlocksY) return VECTRA_SCAN_TOO_LARGE;
+  const int64_t lim = int64_t{1} << 62;
+  if ((a->num_codes > 0 && a->code_stride > lim / a->num_codes) || a->out_stride > lim / a->num_queries ||
+      a->table_stride > lim / a->num_queries)
+    return VECTRA_SCAN_TOO_LARGE;
+  PqAdc p;
+  p.tables = a->tables;
+  p.codes = a->codes;
+  p.ids = a->ids;
+  p.out = a->out;
+  p.table_stride = a->table_stride;
+  p.code_stride = a->code_stride;
+  p.out_stride = a->out_stride;
+  p.num_codes = a->num_codes;
+  p.num_cand = cand;
+  p.subspaces = a->subspaces;
+  p.words = (a->code_stride % 4 == 0 && reinterpret_cast<uintptr_t>(a->codes) % 4 == 0) ? 1 : 0;
+  void* args[] = {&p};
+  const dim3 grid(blocks_for(cand, kThreads), static_cast<unsigned>(a->num_queries));
+  if (a->subspaces <= kMaxLdsTableSubspaces) {
+    const size_t lds = static_cast<size_t>(entries) * sizeof(float);
+    return launched(hipLaunchKernel(reinterpret_cast<const void*>(&pq_adc_kernel<true>), grid, dim3(kThreads), args,
+                                    lds, stream));
+  }
+  return launched(
+      hipLaunchKernel(reinterpret_cast<const void*>(&pq_adc_kernel<false>), grid, dim3(kThreads), args, 0, stream));
+}
+
+extern "C" const char* vectra_scan_status_string(int status) {
+  switch (status) {
+    case VECTRA_SCAN_OK: return "ok";
+    case VECTRA_SCAN_INVALID_ARGUMENT: return "invalid argument";
+    case VECTRA_SCAN_TOO_LARGE: return "problem too large for the scan kernels";
+    case VECTRA_SCAN_LAUNCH_FAILED: return "kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int vectra_scan_abi_version(void) { return VECTRA_SCAN_ABI_VERSION; }

@@ -1,13 +1,15 @@
-"""Locates and loads the two native libraries built in-tree.
+"""Locates and loads the native libraries built in-tree.
 
 * ``libvectra_rbf.so``   -- the C-ABI HIP library (include/vectra_rbf.h);
 * ``libvectra_torch.so`` -- the torch.library extension that registers
-  ``vectra::rbf_attention`` and links the first one.
+  ``vectra::rbf_attention`` and links the first one;
+* ``libvectra_scan.so``  -- the C-ABI distance scans (include/vectra_scan.h),
+  used by vectra_amd.index.
 
-Both are produced by ``make -C vectra_amd/csrc`` (``__graft_entry__.build()``).
-There is no fallback: if they are missing, importing the operator fails.
+All are produced by ``make -C vectra_amd/csrc`` (``__graft_entry__.build()``).
+There is no fallback: if one is missing, the code that needs it fails.
 
-``VECTRA_LIB_DIR`` names another directory holding both libraries; the
+``VECTRA_LIB_DIR`` names another directory holding the libraries; the
 host-sanitizer build (``make -C vectra_amd/csrc sanitize-test``) uses it.
 """
 
@@ -21,6 +23,7 @@ LIB_DIR = os.environ.get('VECTRA_LIB_DIR') or os.path.join(
     os.path.dirname(os.path.dirname(os.path.abspath(__file__))), 'lib')
 HIP_LIBRARY = os.path.join(LIB_DIR, 'libvectra_rbf.so')
 TORCH_LIBRARY = os.path.join(LIB_DIR, 'libvectra_torch.so')
+SCAN_LIBRARY = os.path.join(LIB_DIR, 'libvectra_scan.so')
 
 
 class NativeLibraryMissing(ImportError):
@@ -67,6 +70,21 @@ def hip_library() -> ctypes.CDLL:
     lib.vectra_rbf_status_string.restype = ctypes.c_char_p
     lib.vectra_rbf_abi_version.argtypes = []
     lib.vectra_rbf_abi_version.restype = ctypes.c_int
+    return lib
+
+
+@functools.cache
+def scan_library() -> ctypes.CDLL:
+    """The distance-scan library as a ctypes handle."""
+    lib = ctypes.CDLL(_require(SCAN_LIBRARY))
+    for name in ('vectra_scan_rows', 'vectra_pq_distance_tables', 'vectra_scan_pq_adc'):
+        fn = getattr(lib, name)
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        fn.restype = ctypes.c_int
+    lib.vectra_scan_status_string.argtypes = [ctypes.c_int]
+    lib.vectra_scan_status_string.restype = ctypes.c_char_p
+    lib.vectra_scan_abi_version.argtypes = []
+    lib.vectra_scan_abi_version.restype = ctypes.c_int
     return lib
 
 
