@@ -88,6 +88,9 @@ def parse_args():
     p.add_argument('--sets', type=int, default=0, help='input sets to rotate (0: auto)')
     p.add_argument('--no-read-ceiling', action='store_true',
                    help='skip the plain-read ceiling measurement')
+    p.add_argument('--scan', default=None,
+                   help='benchmark a distance scan of the engine (vectra_amd/benchmarks/scan_workloads.py: '
+                   'flat_shard, flat_shard_q4, exhaustive, pq_shard, pq_tables) instead of the operator')
     return p.parse_args()
 
 
@@ -268,6 +271,154 @@ def load_profile(name):
         return json.load(f)
 
 
+# ---------------------------------------------------------------- scans
+
+REF_SCAN = os.path.join(ROOT, 'oracle', '_ref', 'libref_scan.so')
+SCAN_CPU_ROWS = 65536  # rows (codes, tables) per CPU call and in the numerics sample
+
+
+def _scan_cpu(w, inputs):
+    """(callable computing the workload's outputs for a bounded sample of set
+    0 on the CPU, the sample's output count, kind).  The reference engine's own
+    code (oracle/_ref, built from its sources) where that library is present,
+    else the numpy restatement (oracle/scan.py)."""
+    import numpy as np  # noqa: E402
+
+    from oracle import scan as oracle  # noqa: E402  (cpu_baseline leg only)
+
+    lib = ctypes.CDLL(REF_SCAN) if os.path.exists(REF_SCAN) else None
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    if w.kind == 'rows':
+        rows = inputs['rows'][:SCAN_CPU_ROWS].cpu().numpy()
+        queries = inputs['queries'].cpu().numpy()
+        n = rows.shape[0]
+
+        def run():
+            out = np.empty((queries.shape[0], n), np.float32)
+            for q in range(queries.shape[0]):
+                if lib is not None:
+                    lib.ref_scan_rows(0, ptr(queries[q]), ptr(rows), ctypes.c_int64(n), ctypes.c_int64(w.dim),
+                                      w.dim, ptr(out[q]))
+                else:
+                    out[q] = oracle.l2_squared(queries[q], rows)
+            return out
+        return run, queries.shape[0] * n, ('reference' if lib is not None else 'port')
+    if w.kind == 'adc':
+        codes = np.ascontiguousarray(inputs['codes'][:SCAN_CPU_ROWS].cpu().numpy())
+        tables = inputs['tables'].cpu().numpy()
+        n = codes.shape[0]
+
+        def run():
+            out = np.empty((tables.shape[0], n), np.float32)
+            for q in range(tables.shape[0]):
+                if lib is not None:
+                    lib.ref_pq_adc_rows(ptr(tables[q]), ptr(codes), ctypes.c_int64(n), ctypes.c_int64(w.subspaces),
+                                        w.subspaces, ptr(out[q]))
+                else:
+                    out[q] = oracle.pq_adc(tables[q], codes)
+            return out
+        return run, tables.shape[0] * n, ('reference' if lib is not None else 'port')
+    queries = inputs['queries'][:64].cpu().numpy()
+    books = np.ascontiguousarray(inputs['codebooks'].cpu().numpy())
+
+    def run():
+        out = np.empty((queries.shape[0], w.subspaces * 256), np.float32)
+        for q in range(queries.shape[0]):
+            if lib is not None:
+                assert lib.ref_pq_distance_table(w.dim, w.subspaces, ptr(books), ptr(queries[q]), ptr(out[q])) == 0
+            else:
+                out[q] = oracle.pq_distance_table(queries[q], books, w.subspaces)
+        return out
+    return run, queries.shape[0] * w.subspaces * 256, ('reference' if lib is not None else 'port')
+
+
+def scan_main(args):
+    """`--scan NAME`: one JSON line for a distance scan of the engine."""
+    from vectra_amd.benchmarks import scan_workloads  # noqa: E402
+
+    if args.scan not in scan_workloads.WORKLOADS:
+        raise SystemExit(f'unknown scan workload {args.scan!r}; one of {sorted(scan_workloads.WORKLOADS)}')
+    w = scan_workloads.WORKLOADS[args.scan]
+    sets = scan_workloads.make_sets(w)
+    out = scan_workloads.make_output(w)
+    n_sets = len(sets)
+    log(f'scan {w.name}: {w.set_bytes() / 1e6:.1f} MB per input set, rotating {n_sets} sets')
+    torch.cuda.synchronize()
+
+    # ---- Numerics gate: bit for bit against the CPU on a sample of set 0. ----
+    cpu_run, cpu_outputs, cpu_kind = (None, 0, None)
+    if args.cpu_seconds > 0:
+        import numpy as np  # noqa: E402
+
+        cpu_run, cpu_outputs, cpu_kind = _scan_cpu(w, sets[0])
+        got = scan_workloads.launch(w, sets[0], out)
+        torch.cuda.synchronize()
+        want = cpu_run()
+        got = got[:want.shape[0], :want.shape[1]].cpu().numpy()
+        if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+            raise SystemExit('numerics gate: the scan differs from the CPU reference')
+        log(f'numerics gate passed: {want.size} outputs bit-identical to the {cpu_kind} CPU code')
+
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        scan_workloads.launch(w, sets[i % n_sets], out)
+
+    trial_ms, lead_steps = time_trials(step, args.steps, args.warmup, stream, mode='capi')
+    ms = statistics.median(trial_ms)
+    seconds = ms / 1e3
+
+    cpu = None
+    if cpu_run is not None:
+        cpu_run()
+        reps, start = 0, time.perf_counter()
+        while True:
+            cpu_run()
+            reps += 1
+            elapsed = time.perf_counter() - start
+            if elapsed >= args.cpu_seconds:
+                break
+        what = ("the reference engine's own functions, compiled from its sources" if cpu_kind == 'reference'
+                else 'the numpy restatement of them')
+        cpu = {'value': cpu_outputs * reps / elapsed, 'unit': w.unit, 'cores': 1, 'kind': cpu_kind,
+               'sample': f'{cpu_outputs} outputs of set 0 per call ({what}), one thread, '
+                         f'{reps} calls in {elapsed:.1f}s'}
+        log(f'cpu baseline: {cpu["value"]:.4g} {w.unit} ({cpu_kind})')
+
+    nbytes = w.algorithmic_bytes()
+    achieved = nbytes / seconds / 1e9
+    line_roof = {'bound': 'hbm', 'achieved': achieved, 'peak': roofline.MI355X.hbm_bytes_per_s / 1e9,
+                 'unit': 'GB/s', 'kernel': scan_workloads.KERNEL_NAMES[w.kind], 'traffic': None,
+                 'algorithmic_bytes': nbytes}
+    line_roof['frac'] = achieved / line_roof['peak']
+    measured = load_profile(f'traffic_scan_{w.name}.json')
+    if measured is not None and measured.get('kernel') == line_roof['kernel']:
+        line_roof['traffic'] = measured['traffic_bytes']
+        line_roof['traffic_source'] = f'profiles/traffic_scan_{w.name}.json'
+    if not args.no_read_ceiling and nbytes >= (1 << 20):
+        from vectra_amd.benchmarks import read_ceiling  # noqa: E402
+
+        ceiling = read_ceiling.measure(nbytes)
+        line_roof['read_ceiling'] = {'us': ceiling['us'], 'GB/s': ceiling['GB/s'],
+                                     'frac_of_peak': ceiling['GB/s'] / line_roof['peak'],
+                                     'kernel_over_ceiling': achieved / ceiling['GB/s']}
+        log(f'read ceiling: {ceiling["us"]:.2f} us, {ceiling["GB/s"]:.0f} GB/s')
+    result = {
+        'metric': f'engine distance scan {w.name}: {w.unit} + % of HBM peak',
+        'value': w.outputs_per_launch() / seconds,
+        'unit': w.unit,
+        'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': ms,
+        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32', 'data': 'synthetic',
+        'config': {'workload': f'{w.name}: {w.kind}, queries={w.queries} count={w.count} dim={w.dim} '
+                               f'subspaces={w.subspaces}',
+                   'input_sets': n_sets, 'trials': len(trial_ms), 'lead_in_launches': lead_steps},
+        'roofline': line_roof,
+        'cpu_baseline': cpu,
+        'native_libraries': [os.path.relpath(p, ROOT) for p in _native.loaded_libraries()],
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -280,6 +431,9 @@ def main():
     if not torch.cuda.is_available():
         print('bench.py needs a GPU', file=sys.stderr)
         sys.exit(1)
+    if args.scan:
+        scan_main(args)
+        return
 
     config = configs.CONFIGS[args.config]
     if args.dtype:

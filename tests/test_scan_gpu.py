@@ -147,6 +147,30 @@ def test_adc_scans_against_the_oracle(m):
     _same(got, want, f'adc m {m}')
 
 
+@pytest.mark.parametrize('m', [1, 3, 4, 5, 8, 13, 16, 17, 20, 29, 32])
+def test_adc_short_codes_on_16_byte_boundaries(m):
+    # Codes of <= 32 bytes with a 16-byte-aligned base and stride take the
+    # kernel's 16-byte-load path (the next codes requested before the
+    # current ones are summed).
+    rng = np.random.default_rng(100 + m)
+    n = 5003
+    wide = torch.from_numpy(rng.integers(0, 256, (n, 48), dtype=np.uint8)).cuda()
+    codes = wide[:, :m]                        # stride 48 bytes
+    tables = (rng.standard_normal((2, m * 256)) * 3).astype(np.float32)
+    ids_np = rng.integers(0, n, 1501).astype(np.int32)
+    ids_np[3] = n + 7
+    codes_np = codes.cpu().numpy()
+    got = scan.pq_adc_distances(_gpu(tables), codes)
+    want = np.stack([oracle.pq_adc(tables[i], codes_np) for i in range(2)])
+    _same(got, want, f'aligned adc m {m}')
+    got_ids = scan.pq_adc_distances(_gpu(tables), codes, ids=torch.from_numpy(ids_np).cuda())
+    want_ids = np.full((2, 1501), np.nan, np.float32)
+    ok = ids_np < n
+    for i in range(2):
+        want_ids[i, ok] = oracle.pq_adc(tables[i], codes_np[ids_np[ok]])
+    _same(got_ids, want_ids, f'aligned adc m {m} with ids')
+
+
 def test_adc_with_unaligned_codes_and_ids():
     rng = np.random.default_rng(2)
     n, m = 3000, 16

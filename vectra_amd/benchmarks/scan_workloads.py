@@ -1,0 +1,120 @@
+"""Workloads of the distance-scan benchmark (`python bench.py --scan NAME`).
+
+Sizes follow the reference engine's index configuration
+(engine/configs/hnsw_params.textproto: 128-dimensional float vectors,
+16-byte PQ codes, up to 4,000,000 vectors per shard, exhaustive scans up to
+2,048 rows, re-rank depth 128):
+
+============  ===============================================================
+flat_shard    ShardIndex::ExhaustiveSearch (shard_index.cc:236-264) over a
+              whole shard: L2SquaredDistance of one query to 4,000,000 rows
+flat_shard_q4 the same for four queries at once (each row read once)
+exhaustive    the exhaustive scan the reference actually runs: one query,
+              2,048 rows (exhaustive_scan_threshold)
+pq_shard      PqAdcDistance of one query table over 4,000,000 16-byte codes
+              (the ADC pass of a search over a whole shard)
+pq_tables     ComputeDistanceTable for 1,024 queries (dimension 128,
+              16 sub-spaces)
+============  ===============================================================
+
+Algorithmic bytes per launch count every input byte once and every output
+byte once: rows (or codes, or codebooks), queries (or tables) and the
+distances written.  Inputs rotate over more than the 256 MB Infinity Cache
+where one set is smaller than that.
+"""
+
+import dataclasses
+
+import torch
+
+from vectra_amd.index import scan
+
+ROTATION_BYTES = 320 << 20
+PQ_CENTROIDS = 256
+
+
+@dataclasses.dataclass(frozen=True)
+class Workload:
+    name: str
+    kind: str            # 'rows', 'adc' or 'tables'
+    queries: int
+    count: int           # rows, codes, or (for tables) unused
+    dim: int = 128
+    subspaces: int = 16
+    unit: str = 'distances/s'
+
+    def algorithmic_bytes(self) -> int:
+        if self.kind == 'rows':
+            return self.count * self.dim * 4 + self.queries * self.dim * 4 + self.queries * self.count * 4
+        if self.kind == 'adc':
+            return (self.count * self.subspaces + self.queries * self.subspaces * PQ_CENTROIDS * 4
+                    + self.queries * self.count * 4)
+        # tables: queries + codebooks in, tables out
+        return (self.queries * self.dim * 4 + PQ_CENTROIDS * self.dim * 4
+                + self.queries * self.subspaces * PQ_CENTROIDS * 4)
+
+    def outputs_per_launch(self) -> int:
+        if self.kind == 'tables':
+            return self.queries * self.subspaces * PQ_CENTROIDS
+        return self.queries * self.count
+
+    def set_bytes(self) -> int:
+        if self.kind == 'rows':
+            return self.count * self.dim * 4
+        if self.kind == 'adc':
+            return self.count * self.subspaces
+        return PQ_CENTROIDS * self.dim * 4 + self.queries * self.dim * 4
+
+
+WORKLOADS = {w.name: w for w in (
+    Workload('flat_shard', 'rows', 1, 4_000_000),
+    Workload('flat_shard_q4', 'rows', 4, 4_000_000),
+    Workload('exhaustive', 'rows', 1, 2048),
+    Workload('pq_shard', 'adc', 1, 4_000_000),
+    Workload('pq_tables', 'tables', 1024, 0, unit='table entries/s'),
+)}
+
+KERNEL_NAMES = {'rows': 'scan_rows_kernel', 'adc': 'pq_adc_kernel', 'tables': 'pq_table_kernel'}
+
+
+def sets_needed(w: Workload) -> int:
+    return max(1, min(512, -(-ROTATION_BYTES // max(w.set_bytes(), 1))))
+
+
+def make_sets(w: Workload, seed: int = 0, device='cuda') -> list[dict]:
+    """Input sets on the GPU (float32 normal vectors, uniform codes)."""
+    gen = torch.Generator(device='cpu').manual_seed(seed)
+    n_sets = sets_needed(w)
+    sets = []
+    if w.kind == 'rows':
+        # One host draw, varied per set on the device (scaled), to keep set-up fast.
+        base = torch.randn(w.count, w.dim, generator=gen).to(device)
+        for i in range(n_sets):
+            sets.append({'queries': torch.randn(w.queries, w.dim, generator=gen).to(device),
+                         'rows': base if i == 0 else base * (1.0 + i / 64)})
+    elif w.kind == 'adc':
+        base = torch.randint(0, 256, (w.count, w.subspaces), generator=gen, dtype=torch.uint8).to(device)
+        for i in range(n_sets):
+            sets.append({'tables': (torch.rand(w.queries, w.subspaces * PQ_CENTROIDS, generator=gen) * 8).to(device),
+                         'codes': base if i == 0 else base ^ i})
+    else:
+        for _ in range(n_sets):
+            sets.append({'queries': torch.randn(w.queries, w.dim, generator=gen).to(device),
+                         'codebooks': torch.randn(w.subspaces, PQ_CENTROIDS, w.dim // w.subspaces,
+                                                  generator=gen).to(device)})
+    return sets
+
+
+def make_output(w: Workload, device='cuda') -> torch.Tensor:
+    if w.kind == 'tables':
+        return torch.empty(w.queries, w.subspaces * PQ_CENTROIDS, device=device)
+    return torch.empty(w.queries, w.count, device=device)
+
+
+def launch(w: Workload, inputs: dict, out: torch.Tensor) -> torch.Tensor:
+    """One launch of the workload's kernel on the current stream."""
+    if w.kind == 'rows':
+        return scan.l2_squared_distances(inputs['queries'], inputs['rows'], out=out)
+    if w.kind == 'adc':
+        return scan.pq_adc_distances(inputs['tables'], inputs['codes'], out=out)
+    return scan.pq_distance_tables(inputs['queries'], inputs['codebooks'], w.subspaces, out=out)

@@ -20,7 +20,9 @@
 //   queries.
 // * ADC distances (PqAdcDistance :68-81): one lane per code, four chains over
 //   sub-spaces s .. s + 3, combined as (l0 + l1) + (l2 + l3), then the
-//   remaining sub-spaces; the query's table sits in LDS when it fits.
+//   remaining sub-spaces; the query's table sits in LDS when it fits, and
+//   codes of up to 32 bytes on 16-byte boundaries arrive in 16-byte loads,
+//   the next codes requested before the current ones are summed.
 // * ADC tables (ProductQuantizer::ComputeDistanceTable, pq_codec.cc:208-217):
 //   one lane per (query, sub-space, centroid), the L2 reduction above written
 //   out sequentially in one lane.
@@ -47,6 +49,10 @@ constexpr int kGroupsPerBlock = kThreads / kLanes;
 constexpr int kUnroll = 8;                       // 16-element steps loaded together
 constexpr int kQueryBlock = 4;                   // queries sharing one read of a row
 constexpr int64_t kMaxBlocksX = 1 << 20;         // grid-stride beyond this
+// Scans run on at most this many workgroups (8 per compute unit of an
+// MI355X), each looping over candidates: per-workgroup set-up (query
+// registers, an ADC table in LDS) is paid once for many candidates.
+constexpr int64_t kScanBlocks = 2048;
 constexpr int64_t kMaxBlocksY = 65535;
 constexpr int kMaxLdsTableSubspaces = 64;        // 64 KiB of LDS per table
 
@@ -71,7 +77,7 @@ __device__ __forceinline__ float term(float query, float row) {
   }
 }
 
-template <int kMetric, int kQB>
+template <int kMetric, int kQB, bool kIds>
 __global__ __launch_bounds__(kThreads) void scan_rows_kernel(RowScan p) {
   constexpr bool kNorm = kMetric == VECTRA_SCAN_SQUARED_NORM;
   const int lane = static_cast<int>(threadIdx.x) & (kLanes - 1);
@@ -83,16 +89,18 @@ __global__ __launch_bounds__(kThreads) void scan_rows_kernel(RowScan p) {
   const int tail = p.dim - full;
   // Lane `lane`'s element of query q0 + j is at qlane + j * query_stride.
   const float* qlane = kNorm ? nullptr : p.queries + static_cast<int64_t>(q0) * p.query_stride + lane;
+  // Element i + lane of query q0 + j (the queries stay in the caches).
+  auto query = [&](int j, int i) -> float { return qlane[static_cast<int64_t>(j) * p.query_stride + i]; };
 
   for (int64_t cand = first; cand < p.num_cand; cand += step) {
     int64_t row = cand;
     bool valid = true;
-    if (p.ids != nullptr) {
+    if constexpr (kIds) {
       const uint32_t id = p.ids[cand];
       valid = static_cast<int64_t>(id) < p.num_rows;
-      row = id;
+      row = valid ? id : 0;
     }
-    const float* rlane = p.rows + (valid ? row : 0) * p.row_stride + lane;
+    const float* rlane = p.rows + row * p.row_stride + lane;
     float acc[kQB];
 #pragma unroll
     for (int j = 0; j < kQB; ++j) acc[j] = 0.f;
@@ -107,8 +115,7 @@ __global__ __launch_bounds__(kThreads) void scan_rows_kernel(RowScan p) {
           if (j < nq) {
             float qv[kUnroll];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u)
-              qv[u] = kNorm ? rv[u] : qlane[static_cast<int64_t>(j) * p.query_stride + i + kLanes * u];
+            for (int u = 0; u < kUnroll; ++u) qv[u] = kNorm ? rv[u] : query(j, i + kLanes * u);
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) acc[j] = acc[j] + term<kMetric>(qv[u], rv[u]);
           }
@@ -118,13 +125,11 @@ __global__ __launch_bounds__(kThreads) void scan_rows_kernel(RowScan p) {
         const float r = rlane[i];
 #pragma unroll
         for (int j = 0; j < kQB; ++j) {
-          if (j < nq) {
-            const float q = kNorm ? r : qlane[static_cast<int64_t>(j) * p.query_stride + i];
-            acc[j] = acc[j] + term<kMetric>(q, r);
-          }
+          if (j < nq) acc[j] = acc[j] + term<kMetric>(kNorm ? r : query(j, i), r);
         }
       }
     }
+    const float rtail = valid && lane < tail ? rlane[full] : 0.f;
 #pragma unroll
     for (int j = 0; j < kQB; ++j) {
       if (j >= nq) break;
@@ -137,10 +142,7 @@ __global__ __launch_bounds__(kThreads) void scan_rows_kernel(RowScan p) {
       }
       // The tail, element by element in order (lane k holds element full + k).
       float t = 0.f;
-      if (valid && lane < tail) {
-        const float r = rlane[full];
-        t = term<kMetric>(kNorm ? r : qlane[static_cast<int64_t>(j) * p.query_stride + full], r);
-      }
+      if (valid && lane < tail) t = term<kMetric>(kNorm ? rtail : query(j, full), rtail);
       for (int k = 0; k < tail; ++k) sum = sum + __shfl(t, k, kLanes);
       if (lane == 0) p.out[static_cast<int64_t>(q0 + j) * p.out_stride + cand] = valid ? sum : NAN;
     }
@@ -256,25 +258,132 @@ __global__ __launch_bounds__(kThreads) void pq_adc_kernel(PqAdc p) {
   }
 }
 
-unsigned blocks_for(int64_t items, int per_block) {
+// The ADC scan for codes of at most 32 bytes laid out on 16-byte boundaries
+// (base and stride): a code arrives in kChunks 16-byte loads, each lane
+// takes kAdcCodes codes per round and requests the next round's codes before
+// summing the current ones, and the table sits in LDS.  The sums are
+// adc_sum's, on the code's words.  (Two codes per round: four held 64 VGPRs
+// and ran slower at the lower occupancy.)
+constexpr int kAdcCodes = 2;
+
+template <int kChunks, typename Entry>
+__device__ __forceinline__ float adc_sum_words(const uint4 (&chunk)[kChunks], int m, Entry entry) {
+  constexpr int kWords = 4 * kChunks;
+  uint32_t words[kWords];
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    words[4 * c] = chunk[c].x;
+    words[4 * c + 1] = chunk[c].y;
+    words[4 * c + 2] = chunk[c].z;
+    words[4 * c + 3] = chunk[c].w;
+  }
+  float l0 = 0.f, l1 = 0.f, l2 = 0.f, l3 = 0.f;
+#pragma unroll
+  for (int k = 0; k < kWords; ++k) {
+    if (4 * k + 4 <= m) {
+      const uint32_t w = words[k];
+      l0 = l0 + entry(4 * k, w & 0xffu);
+      l1 = l1 + entry(4 * k + 1, (w >> 8) & 0xffu);
+      l2 = l2 + entry(4 * k + 2, (w >> 16) & 0xffu);
+      l3 = l3 + entry(4 * k + 3, w >> 24);
+    }
+  }
+  float sum = (l0 + l1) + (l2 + l3);
+  const int full = m & ~3;
+  uint32_t last = 0;
+#pragma unroll
+  for (int k = 0; k < kWords; ++k)
+    if (k == full / 4) last = words[k];
+#pragma unroll
+  for (int r = 0; r < 3; ++r)
+    if (full + r < m) sum = sum + entry(full + r, (last >> (8 * r)) & 0xffu);
+  return sum;
+}
+
+template <int kChunks>
+__global__ __launch_bounds__(kThreads) void pq_adc_vec_kernel(PqAdc p) {
+  extern __shared__ float table_lds[];  // subspaces * 256 floats
+  const int64_t q = blockIdx.y;
+  const float* table = p.tables + q * p.table_stride;
+  const int m = p.subspaces;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  // Codes base + k * stride, k < kAdcCodes: valid flags and 16-byte chunks.
+  auto load = [&](int64_t base, bool (&valid)[kAdcCodes], uint4 (&chunk)[kAdcCodes][kChunks]) {
+    // All candidate ids first, so their latencies overlap.
+    uint32_t id[kAdcCodes];
+#pragma unroll
+    for (int k = 0; k < kAdcCodes; ++k) {
+      const int64_t cand = base + k * stride;
+      id[k] = p.ids != nullptr && cand < p.num_cand ? p.ids[cand] : 0u;
+    }
+#pragma unroll
+    for (int k = 0; k < kAdcCodes; ++k) {
+      const int64_t cand = base + k * stride;
+      int64_t index = cand;
+      valid[k] = cand < p.num_cand;
+      if (p.ids != nullptr) {
+        valid[k] = valid[k] && static_cast<int64_t>(id[k]) < p.num_codes;
+        index = id[k];
+      }
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c)
+        chunk[k][c] = valid[k] ? *reinterpret_cast<const uint4*>(p.codes + index * p.code_stride + 16 * c)
+                               : make_uint4(0, 0, 0, 0);
+    }
+  };
+  // The first codes are requested before the table is staged, and each
+  // round requests the next round's codes before summing its own.
+  int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  bool valid[kAdcCodes];
+  uint4 chunk[kAdcCodes][kChunks];
+  load(base, valid, chunk);
+  for (int i = static_cast<int>(threadIdx.x); i < m * VECTRA_PQ_CENTROIDS; i += kThreads) table_lds[i] = table[i];
+  __syncthreads();
+  auto entry = [&](int s, uint32_t c) { return table_lds[s * VECTRA_PQ_CENTROIDS + static_cast<int>(c)]; };
+  for (; base < p.num_cand; base += stride * kAdcCodes) {
+    bool next_valid[kAdcCodes];
+    uint4 next[kAdcCodes][kChunks];
+    load(base + stride * kAdcCodes, next_valid, next);
+#pragma unroll
+    for (int k = 0; k < kAdcCodes; ++k) {
+      const int64_t cand = base + k * stride;
+      if (cand < p.num_cand) p.out[q * p.out_stride + cand] = valid[k] ? adc_sum_words(chunk[k], m, entry) : NAN;
+    }
+#pragma unroll
+    for (int k = 0; k < kAdcCodes; ++k) {
+      valid[k] = next_valid[k];
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c) chunk[k][c] = next[k][c];
+    }
+  }
+}
+
+unsigned blocks_for(int64_t items, int per_block, int64_t cap = kMaxBlocksX) {
   int64_t blocks = (items + per_block - 1) / per_block;
-  if (blocks > kMaxBlocksX) blocks = kMaxBlocksX;
+  if (blocks > cap) blocks = cap;
   return static_cast<unsigned>(blocks < 1 ? 1 : blocks);
 }
 
 int launched(hipError_t e) { return e == hipSuccess ? VECTRA_SCAN_OK : VECTRA_SCAN_LAUNCH_FAILED; }
 
-template <int kMetric>
-int launch_rows(const RowScan& p, hipStream_t stream) {
-  void* args[] = {const_cast<RowScan*>(&p)};
+template <int kMetric, bool kIds>
+int launch_rows_ids(RowScan& p, hipStream_t stream) {
+  void* args[] = {&p};
+  // One pass of the grid covers every candidate: a wave's row loads are then
+  // never queued behind its previous candidate's fold.
   const unsigned bx = blocks_for(p.num_cand, kGroupsPerBlock);
   if (p.num_queries == 1 || kMetric == VECTRA_SCAN_SQUARED_NORM) {
-    return launched(hipLaunchKernel(reinterpret_cast<const void*>(&scan_rows_kernel<kMetric, 1>), dim3(bx, 1),
+    return launched(hipLaunchKernel(reinterpret_cast<const void*>(&scan_rows_kernel<kMetric, 1, kIds>), dim3(bx, 1),
                                     dim3(kThreads), args, 0, stream));
   }
   const unsigned by = static_cast<unsigned>((p.num_queries + kQueryBlock - 1) / kQueryBlock);
-  return launched(hipLaunchKernel(reinterpret_cast<const void*>(&scan_rows_kernel<kMetric, kQueryBlock>),
+  return launched(hipLaunchKernel(reinterpret_cast<const void*>(&scan_rows_kernel<kMetric, kQueryBlock, kIds>),
                                   dim3(bx, by), dim3(kThreads), args, 0, stream));
+}
+
+template <int kMetric>
+int launch_rows(RowScan& p, hipStream_t stream) {
+  return p.ids != nullptr ? launch_rows_ids<kMetric, true>(p, stream) : launch_rows_ids<kMetric, false>(p, stream);
 }
 
 }  // namespace
@@ -377,7 +486,14 @@ extern "C" int vectra_scan_pq_adc(const vectra_pq_adc_args* a, hipStream_t strea
   p.subspaces = a->subspaces;
   p.words = (a->code_stride % 4 == 0 && reinterpret_cast<uintptr_t>(a->codes) % 4 == 0) ? 1 : 0;
   void* args[] = {&p};
-  const dim3 grid(blocks_for(cand, kThreads), static_cast<unsigned>(a->num_queries));
+  const dim3 grid(blocks_for(cand, kThreads, kScanBlocks), static_cast<unsigned>(a->num_queries));
+  const bool vec16 = a->code_stride % 16 == 0 && reinterpret_cast<uintptr_t>(a->codes) % 16 == 0;
+  if (vec16 && a->subspaces <= 32) {
+    const size_t lds = static_cast<size_t>(entries) * sizeof(float);
+    const void* kernel = a->subspaces <= 16 ? reinterpret_cast<const void*>(&pq_adc_vec_kernel<1>)
+                                            : reinterpret_cast<const void*>(&pq_adc_vec_kernel<2>);
+    return launched(hipLaunchKernel(kernel, grid, dim3(kThreads), args, lds, stream));
+  }
   if (a->subspaces <= kMaxLdsTableSubspaces) {
     const size_t lds = static_cast<size_t>(entries) * sizeof(float);
     return launched(hipLaunchKernel(reinterpret_cast<const void*>(&pq_adc_kernel<true>), grid, dim3(kThreads), args,
