@@ -1,0 +1,179 @@
+"""A CPU model of the 16-bit matrix-core kernels' own numerics (test
+infrastructure; it models this repository's kernels, not the reference).
+
+rbf_plane_kernel (vectra_amd/csrc/rbf_plane_impl.h) and rbf_tile_kernel
+(rbf_tile_impl.h) do not follow the reference's online-softmax algorithm.
+For bf16/fp16 inputs they compute, per (b, h) plane, in fp32:
+
+  coef = (2 log2 e) * gamma
+  c_j  = fma(-coef / 2, |k_j|^2, log2(e) * bias_j)              (-inf masked)
+  plane: x_ij = fma(coef, q_i . k_j,               c_j - shift_i)
+  tile:  x_ij = fma(coef, q_i . k_j - |q_i|^2 / 2, c_j) - shift_i
+  w = exp2(x); hi = 16-bit(w); lo = 16-bit(w - hi)   (bf16 round to nearest,
+                                                      fp16 round toward zero)
+  total_i = sum_j (hi + lo);  acc_i = sum_j hi v_j + sum_j lo v_j
+  out_i = acc_i * (1 / total_i)
+
+with no clamp of the distance at 0 and no running maximum: shift_i = 0
+unless the weight sums leave the range where the split is accurate
+([2^-32, 2^32] for bf16, [2^-3, 2^15] for fp16).  The plane kernel tests the
+16 queries of a block together and recomputes the whole block with each
+query's own maximum logit subtracted; the tile kernel takes the exact passes
+(a maximum pass, then a shifted pass) for every query of its work item when
+a bias is present, gamma < 0, or any sum falls below the range.
+
+Sums here are taken in float64 and rounded once (the matrix cores' order of
+accumulation is not modelled), so the kernels match this model to ~1e-6
+relative, not bit for bit.  tests/test_kernel_model.py bounds the model's
+error against the fp64 oracle on the CPU, including both branches;
+tests/test_kernel_model_gpu.py checks the kernels against the model.
+"""
+
+import numpy as np
+
+F32 = np.float32
+LOG2E = F32(1.4426950408889634)
+TWO_LOG2E = F32(2.0) * LOG2E
+SUM_RANGE = {'bf16': (F32(2.0 ** -32), F32(2.0 ** 32)), 'fp16': (F32(2.0 ** -3), F32(2.0 ** 15))}
+TILE_ITEM_ROWS = 128  # query rows of one tile-kernel work item (4 waves x 2 blocks x 16)
+
+
+def to_bf16(x):
+    """Round float32 values to bf16 (nearest, ties to even), as float32."""
+    x = np.asarray(x, dtype=F32)
+    bits = x.view(np.uint32).astype(np.uint64)
+    rounded = ((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    out = rounded.view(F32)
+    return np.where(np.isnan(x), x, out).astype(F32)
+
+
+def to_fp16_rtz(x):
+    """Round float32 values to fp16 toward zero (v_cvt_pkrtz), as float32."""
+    x = np.asarray(x, dtype=F32)
+    with np.errstate(over='ignore'):
+        h = x.astype(np.float16)
+    too_far = np.abs(h.astype(F32)) > np.abs(x)
+    h = np.where(too_far, np.nextafter(h, np.float16(0)), h)
+    return h.astype(F32)
+
+
+def split(w, kind):
+    """(hi, lo) of the weights: hi + lo = w to ~2^-17 (bf16) / 2^-20 (fp16)."""
+    rnd = to_bf16 if kind == 'bf16' else to_fp16_rtz
+    hi = rnd(w)
+    with np.errstate(invalid='ignore'):
+        lo = rnd((w - hi).astype(F32))
+    return hi, lo
+
+
+def fma32(a, b, c):
+    """fp32 fused multiply-add (the product is exact in float64)."""
+    with np.errstate(invalid='ignore', over='ignore'):
+        return (np.asarray(a, np.float64) * np.asarray(b, np.float64) + np.asarray(c, np.float64)).astype(F32)
+
+
+def exp2_32(x):
+    with np.errstate(over='ignore'):
+        return np.exp2(np.asarray(x, np.float64)).astype(F32)
+
+
+def _weighted(x, shift, v, kind):
+    """(acc [n, dv], total [n]) of logits x [n, nk] with per-row shifts."""
+    w = exp2_32((x - shift[:, None]).astype(F32) if shift is not None else x)
+    hi, lo = split(w, kind)
+    v64 = v.astype(np.float64)
+    with np.errstate(invalid='ignore', over='ignore'):
+        acc = (hi.astype(np.float64) @ v64 + lo.astype(np.float64) @ v64).astype(F32)
+        total = (hi.astype(np.float64) + lo.astype(np.float64)).sum(-1).astype(F32)
+    return acc, total
+
+
+def _row_max(x):
+    m = x.max(-1) if x.shape[-1] else np.full(x.shape[0], -np.inf, F32)
+    return np.where(np.isneginf(m), F32(0), m).astype(F32)
+
+
+def _in_range(total, kind):
+    lo, hi = SUM_RANGE[kind]
+    return (total >= lo) & (total <= hi)  # False for NaN
+
+
+def _finish(acc, total):
+    with np.errstate(divide='ignore', invalid='ignore'):
+        inv = (F32(1) / total).astype(F32)
+        return (acc * inv[:, None]).astype(F32)
+
+
+def _folded_keys(k, gamma, bias):
+    coef = F32(TWO_LOG2E * F32(gamma))
+    sq = (k.astype(np.float64) ** 2).sum(-1).astype(F32)
+    xb = np.zeros(k.shape[0], F32) if bias is None else (np.asarray(bias, F32) * LOG2E).astype(F32)
+    return coef, fma32(F32(-0.5) * coef, sq, xb)
+
+
+def plane(q, k, v, gamma, bias, kind, one_pass=False):
+    """rbf_plane_kernel on one plane: q [nq, d], k [nk, d], v [nk, dv] (values
+    already in the 16-bit type), gamma, bias [nk] or None.  Returns (out
+    [nq, dv] float32, per-query flags of the shifted recompute)."""
+    q, k, v = (np.asarray(a, F32) for a in (q, k, v))
+    coef, c = _folded_keys(k, gamma, bias)
+    s = (q.astype(np.float64) @ k.astype(np.float64).T).astype(F32)
+    nq = q.shape[0]
+    out = np.zeros((nq, v.shape[1]), F32)
+    shifted = np.zeros(nq, bool)
+    for b0 in range(0, nq, 16):
+        rows = slice(b0, min(b0 + 16, nq))
+        x0 = fma32(coef, s[rows], c[None, :])
+        acc, total = _weighted(x0, None, v, kind)
+        if not one_pass and not _in_range(total, kind).all():
+            shift = _row_max(x0)
+            x = fma32(coef, s[rows], (c[None, :] - shift[:, None]).astype(F32))
+            acc, total = _weighted(x, None, v, kind)
+            shifted[rows] = True
+        out[rows] = _finish(acc, total)
+    return out, shifted
+
+
+def tile(q, k, v, gamma, bias, kind, one_pass=False):
+    """rbf_tile_kernel on one plane (work items of 128 query rows); same
+    arguments and results as `plane`."""
+    q, k, v = (np.asarray(a, F32) for a in (q, k, v))
+    coef, c = _folded_keys(k, gamma, bias)
+    nq = q.shape[0]
+    half_q = (F32(-0.5) * (q.astype(np.float64) ** 2).sum(-1).astype(F32)).astype(F32)
+    s = ((q.astype(np.float64) @ k.astype(np.float64).T) + half_q[:, None].astype(np.float64)).astype(F32)
+    out = np.zeros((nq, v.shape[1]), F32)
+    shifted = np.zeros(nq, bool)
+    exact_always = bias is not None or not (coef >= 0)
+    for r0 in range(0, nq, TILE_ITEM_ROWS):
+        rows = slice(r0, min(r0 + TILE_ITEM_ROWS, nq))
+        x0 = fma32(coef, s[rows], c[None, :])
+        exact = exact_always and not one_pass
+        if not exact:
+            acc, total = _weighted(x0, None, v, kind)
+            lo = SUM_RANGE[kind][0]
+            exact = not one_pass and not (total >= lo).all()
+        if exact:
+            acc, total = _weighted(x0, _row_max(x0), v, kind)
+            shifted[rows] = True
+        out[rows] = _finish(acc, total)
+    return out, shifted
+
+
+def run(model, q, k, v, scale, bias, kind, one_pass=False):
+    """A model over [B, H, n, d] torch or numpy operands with the operator's
+    broadcasting (scale [1|B, 1|H, 1, 1] or a scalar; bias [B, 1|H, 1, nk] or
+    None).  Returns (out [B, H, nq, dv] float32, shifted [B, H, nq])."""
+    q, k, v = (np.asarray(a, F32) for a in (q, k, v))
+    batch, heads, nq, _ = q.shape
+    sc = np.asarray(scale, F32)
+    sc = np.broadcast_to(sc.reshape(sc.shape[:2]) if sc.ndim == 4 else sc.reshape(1, 1), (batch, heads))
+    bs = None if bias is None else np.broadcast_to(np.asarray(bias, F32)[:, :, 0, :], (batch, heads, k.shape[2]))
+    fn = plane if model == 'plane' else tile
+    out = np.zeros((batch, heads, nq, v.shape[-1]), F32)
+    shifted = np.zeros((batch, heads, nq), bool)
+    for b in range(batch):
+        for h in range(heads):
+            out[b, h], shifted[b, h] = fn(q[b, h], k[b, h], v[b, h], sc[b, h],
+                                          None if bs is None else bs[b, h], kind, one_pass)
+    return out, shifted

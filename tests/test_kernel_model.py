@@ -1,0 +1,160 @@
+"""The plane and tile kernels' own numerics, modelled on the CPU
+(tests/kernel_model.py), against the fp64 oracle.
+
+The kernels replace the reference's online softmax with unshifted exp2 and a
+range check, feed the weights as 16-bit hi + lo pairs and drop the clamp of
+the expanded distance at 0.  These tests run that design on the CPU over the
+16-bit edge cases and over the regime where dropping the clamp matters most
+(large norms with a large gamma), so its error is bounded before any GPU
+run; tests/test_kernel_model_gpu.py then holds the kernels to the model.
+"""
+
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rbf as oracle
+from tests import kernel_model as km
+from tests.half_cases import HALF_CASES, HALF_KERNEL_SHAPES, half_case
+
+HALF_TOL = {'rtol': 1e-3, 'atol': 1e-4}
+KINDS = {'bf16': torch.bfloat16, 'fp16': torch.float16}
+
+
+def _case(case, shape, kind):
+    n_q, n_k, dim = HALF_KERNEL_SHAPES[shape]
+    gen = torch.Generator().manual_seed(zlib.crc32(f'{case}/{shape}'.encode()) % 1000)
+    q, k, v, scale, bias = half_case(case, n_q, n_k, dim, gen)
+    dt = KINDS[kind]
+    return q.to(dt).float(), k.to(dt).float(), v.to(dt).float(), scale, bias
+
+
+@pytest.mark.parametrize('kind', sorted(KINDS))
+@pytest.mark.parametrize('shape', sorted(HALF_KERNEL_SHAPES))
+@pytest.mark.parametrize('case', HALF_CASES)
+def test_the_design_meets_the_gate_on_the_edge_cases(case, shape, kind):
+    q, k, v, scale, bias = _case(case, shape, kind)
+    model = 'plane' if shape.startswith('plane') else 'tile'
+    got, _ = km.run(model, q, k, v, scale, bias, kind)
+    want = oracle.expanded_fp64(q, k, v, scale, bias)
+    np.testing.assert_allclose(got, want, equal_nan=True, **HALF_TOL)
+
+
+def test_both_branches_are_taken():
+    """The shifted recompute runs exactly where the unshifted weights leave
+    the accurate range, and not on ordinary inputs."""
+    seen = {}
+    for kind in KINDS:
+        for case in HALF_CASES:
+            for shape in ('plane32', 'tile32'):
+                q, k, v, scale, bias = _case(case, shape, kind)
+                _, shifted = km.run(shape[:-2], q, k, v, scale, bias, kind)
+                seen[(kind, case, shape)] = shifted.mean()
+    for kind in KINDS:
+        # Far points: the weights underflow unshifted (a block is recomputed
+        # when any of its 16 queries leaves the range).
+        assert seen[(kind, 'far_points', 'plane32')] >= 0.9
+        assert seen[(kind, 'far_points', 'tile32')] == 1.0
+        # Biases of +-40: far outside both ranges.
+        assert seen[(kind, 'large_biases', 'plane32')] == 1.0
+        # Fully masked rows (sum 0) are recomputed, to NaN; the others not.
+        assert seen[(kind, 'fully_masked', 'plane32')] == 0.5
+        # Ordinary inputs stay unshifted in the plane kernel.
+        for case in ('negative_scale', 'zero_scale', 'one_live_key', 'ragged_mask'):
+            assert seen[(kind, case, 'plane32')] == 0.0, case
+        # The tile kernel's single pass needs no bias and gamma >= 0.
+        for case in ('negative_scale', 'zero_scale', 'ragged_mask'):
+            assert seen[(kind, case, 'tile32')] == 1.0, case
+        q, k, v, _, _ = _case('ragged_mask', 'tile32', kind)
+        assert not km.run('tile', q, k, v, torch.tensor(0.01), None, kind)[1].any()
+
+
+# Cases where one unshifted pass misses the gate: weights that overflow
+# (biases of +-40) or underflow to a 0 / 0 sum (far points in the tile kernel,
+# whose logits are <= 0 by construction).
+ONE_PASS_FAILS = {
+    'bf16': [('large_biases', 'plane16'), ('large_biases', 'tile32'), ('far_points', 'tile64')],
+    'fp16': [('large_biases', 'plane16'), ('large_biases', 'plane32'), ('large_biases', 'tile64'),
+             ('far_points', 'plane32'), ('far_points', 'tile32')],
+}
+
+
+@pytest.mark.parametrize('kind', sorted(KINDS))
+def test_the_range_check_is_needed(kind):
+    """Where the model recomputes, one unshifted pass would miss the gate on
+    these cases, so the check is not decorative."""
+    for case, shape in ONE_PASS_FAILS[kind]:
+        q, k, v, scale, bias = _case(case, shape, kind)
+        model = 'plane' if shape.startswith('plane') else 'tile'
+        want = oracle.expanded_fp64(q, k, v, scale, bias)
+        one, _ = km.run(model, q, k, v, scale, bias, kind, one_pass=True)
+        with np.errstate(invalid='ignore'):
+            bad = ~np.isclose(one, want, equal_nan=True, **HALF_TOL)
+        assert bad.mean() > 0.1, (case, shape)
+
+
+def test_split_precision():
+    """hi + lo keeps ~2^-17 of a bf16-split weight anywhere in fp32's range;
+    fp16 keeps 2^-20 of weights in [2^-3, 2^15) and an absolute 2^-24 below
+    (its subnormal step), which the range check's sum >= 2^-3 makes
+    relative 2^-21 of the sum."""
+    rng = np.random.default_rng(0)
+    w = np.exp2(rng.uniform(-100, 30, 200000)).astype(np.float32)
+    hi, lo = km.split(w, 'bf16')
+    assert (np.abs((hi.astype(np.float64) + lo) - w) / w).max() <= 2.0 ** -16
+    w = np.exp2(rng.uniform(-30, 14.9, 200000)).astype(np.float32)
+    hi, lo = km.split(w, 'fp16')
+    err = np.abs((hi.astype(np.float64) + lo) - w)
+    normal = w >= 2.0 ** -3
+    assert (err[normal] / w[normal]).max() <= 2.0 ** -20
+    assert err[~normal].max() <= 2.0 ** -24
+    # Round toward zero: hi never exceeds w, and lo >= 0.
+    assert (hi <= w).all() and (lo >= 0).all()
+
+
+def _large_norm_case(seed, norm, gamma, n_q=40, n_k=65, dim=32, kind='bf16'):
+    """A cluster of keys of radius ~1 around a centre of norm `norm`, and
+    queries inside it: the distances are O(1), so the weights are spread
+    (gamma d of a few units), while |q|^2 + |k|^2 is ~2 norm^2, so the
+    expansion |q|^2 + |k|^2 - 2 q.k cancels ~2 norm^2 down to O(1)."""
+    gen = torch.Generator().manual_seed(seed)
+    centre = torch.randn(dim, generator=gen)
+    centre = centre / centre.norm() * norm
+    k = centre + torch.randn(1, 1, n_k, dim, generator=gen) / dim ** 0.5
+    q = centre + torch.randn(1, 1, n_q, dim, generator=gen) / dim ** 0.5
+    v = torch.randn(1, 1, n_k, dim, generator=gen)
+    dt = KINDS[kind]
+    return q.to(dt).float(), k.to(dt).float(), v.to(dt).float(), torch.tensor(gamma), None
+
+
+@pytest.mark.parametrize('kind', sorted(KINDS))
+@pytest.mark.parametrize('norm,gamma', [(3.0, 2.0), (10.0, 2.0), (30.0, 2.0), (100.0, 2.0), (100.0, 0.5)])
+def test_dropping_the_clamp_costs_no_more_than_the_expansion_error(kind, norm, gamma):
+    """Large norms with a large gamma, where the clamp's effect is largest.
+
+    Without the clamp the kernels' logit for key j differs from the
+    reference's clamped one only where the rounded expansion is negative,
+    and then by gamma |d~| with |d~| <= (D + 2) u (|q|^2 + |k|^2) (u = 2^-24,
+    the standard bound of a D-term fp32 dot product): the same size as the
+    expansion's own rounding error, which the reference's fp32 kernel
+    (reproduced by oracle.tiled in fp32, with its clamp) carries as well.  So
+    the model's error against fp64 is held to that of the reference's
+    algorithm in fp32, plus the 16-bit split's share."""
+    q, k, v, scale, bias = _large_norm_case(int(norm * 7 + gamma * 100), norm, gamma, kind=kind)
+    want = oracle.direct_fp64(q, k, v, scale, bias)
+    ref32 = oracle.tiled(q, k, v, scale, bias, dtype=np.float32)
+    ref_err = np.abs(ref32 - want).max()
+    for model in ('plane', 'tile'):
+        got, _ = km.run(model, q, k, v, scale, bias, kind)
+        err = np.abs(got - want).max()
+        assert err <= 2 * ref_err + 1e-5, (model, err, ref_err)
+    # The bound itself, per logit, on these inputs.
+    dim = q.shape[-1]
+    qn = (q.double() ** 2).sum(-1)[..., :, None]
+    kn = (k.double() ** 2).sum(-1)[..., None, :]
+    bound = gamma * (dim + 2) * 2.0 ** -24 * (qn + kn)
+    d32 = (qn.float() + kn.float() - 2 * q @ k.transpose(-1, -2)).double()
+    d64 = ((q.double()[..., :, None, :] - k.double()[..., None, :, :]) ** 2).sum(-1)
+    assert (gamma * (d32 - d64).abs() <= bound).all()

@@ -1,0 +1,72 @@
+"""The plane and tile kernels against the CPU model of their own numerics
+(tests/kernel_model.py), on the GPU.
+
+The model takes its sums in float64 and rounds once, while the matrix cores
+accumulate in their own order; with logits of a few hundred (far points) a
+float32 ulp of q.k moves a weight by ~2e-5 of itself.  So the two agree to
+rtol 1e-4 / atol 2e-5: ten times inside the 1e-3 / 1e-4 gate, and twenty
+times below what a dropped lo part (2^-9 of every weight), a missed
+recompute (0 / 0 or overflow) or a wrong folded key value would change.  The
+cases are the 16-bit edge cases, which drive both kernels through both
+branches, and, against fp64, the large-norm cases where dropping the clamp matters
+most.
+"""
+
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rbf as oracle
+from tests import kernel_model as km
+from tests.half_cases import HALF_CASES, HALF_KERNEL_SHAPES, half_case
+from tests.test_kernel_model import _large_norm_case
+from vectra_amd.kernels import capi
+
+pytestmark = pytest.mark.gpu
+
+MODEL_TOL = {'rtol': 1e-4, 'atol': 2e-5}
+KINDS = {'bf16': torch.bfloat16, 'fp16': torch.float16}
+
+
+def _kernel(q, k, v, scale, bias, dtype, variant):
+    out = capi.forward(q.to('cuda', dtype), k.to('cuda', dtype), v.to('cuda', dtype), scale.cuda(),
+                       None if bias is None else bias.cuda(), out_dtype=torch.float32, variant=variant)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize('kind', sorted(KINDS))
+@pytest.mark.parametrize('shape', sorted(HALF_KERNEL_SHAPES))
+@pytest.mark.parametrize('case', HALF_CASES)
+def test_kernels_follow_the_model(case, shape, kind):
+    n_q, n_k, dim = HALF_KERNEL_SHAPES[shape]
+    gen = torch.Generator().manual_seed(zlib.crc32(f'{case}/{shape}'.encode()) % 1000)
+    q, k, v, scale, bias = half_case(case, n_q, n_k, dim, gen)
+    dt = KINDS[kind]
+    q, k, v = q.to(dt).float(), k.to(dt).float(), v.to(dt).float()
+    variant = 'plane' if shape.startswith('plane') else 'tile'
+    print(f'case={case} shape={shape} kind={kind} variant={variant}', flush=True)
+    want, _ = km.run(variant, q, k, v, scale, bias, kind)
+    got = _kernel(q, k, v, scale, bias, dt, variant)
+    np.testing.assert_allclose(got, want, equal_nan=True, **MODEL_TOL)
+
+
+@pytest.mark.parametrize('kind', sorted(KINDS))
+@pytest.mark.parametrize('norm,gamma', [(10.0, 2.0), (30.0, 2.0), (100.0, 2.0), (100.0, 0.5)])
+def test_large_norms_without_the_clamp(kind, norm, gamma):
+    """Where the dropped clamp matters most, the kernels err against fp64 no
+    more than the reference's algorithm does in fp32 (oracle.tiled, with its
+    clamp).  (Here the logits are differences of terms ~2 norm^2 apart, so
+    float32 accumulation order alone moves them by ~1e-3: the kernels are
+    held to the error bound, not to the model's float64 sums.)"""
+    q, k, v, scale, bias = _large_norm_case(int(norm * 7 + gamma * 100), norm, gamma, kind=kind)
+    want = oracle.direct_fp64(q, k, v, scale, bias)
+    ref_err = np.abs(oracle.tiled(q, k, v, scale, bias, dtype=np.float32) - want).max()
+    for variant in ('plane', 'tile'):
+        got = _kernel(q, k, v, scale, bias, KINDS[kind], variant)
+        err = np.abs(got - want).max()
+        print(f'norm={norm} gamma={gamma} kind={kind} variant={variant}: error {err:.3g}, '
+              f'reference algorithm in fp32 {ref_err:.3g}', flush=True)
+        assert err <= 2 * ref_err + 1e-5

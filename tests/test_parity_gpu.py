@@ -17,6 +17,7 @@ import torch
 
 from oracle import rbf as oracle
 from tests import _golden
+from tests.half_cases import HALF_CASES, HALF_KERNEL_SHAPES, half_case as _half_case
 from vectra_amd.benchmarks import configs
 from vectra_amd.kernels import _native
 from vectra_amd.kernels import capi
@@ -370,41 +371,7 @@ def test_two_byte_bias_planes_at_any_alignment(bias_dtype, n_q):
 # Shapes that reach the 16-bit query-tile kernels: one plane tile per wave
 # (head dims 16 and 32, <= 80 rows) and streamed key tiles (more keys, or
 # 64-dim heads).
-HALF_KERNEL_SHAPES = {'plane16': (24, 70, 16), 'plane32': (40, 65, 32), 'tile32': (40, 200, 32),
-                      'tile64': (33, 130, 64)}
-
-
-def _half_case(case, n_q, n_k, dim, gen):
-    q = torch.randn(2, 2, n_q, dim, generator=gen)
-    k = torch.randn(2, 2, n_k, dim, generator=gen)
-    v = torch.randn(2, 2, n_k, dim, generator=gen)
-    scale, bias = torch.tensor(0.5 / dim), None
-    if case == 'far_points':
-        # Every key far from every query (gamma d of a few hundred), so the
-        # weights underflow unless each query's largest logit is subtracted;
-        # distances stay where fp32 resolves them to the tolerance.
-        q, k, scale = q * 3, k * 3, torch.tensor(0.3)
-    elif case == 'negative_scale':
-        scale = torch.tensor(-0.01)
-    elif case == 'zero_scale':
-        scale = torch.tensor(0.0)
-        bias = torch.randn(2, 1, 1, n_k, generator=gen)
-    elif case == 'fully_masked':
-        bias = torch.zeros(2, 1, 1, n_k)
-        bias[1] = -math.inf
-    elif case == 'one_live_key':
-        bias = torch.full((2, 1, 1, n_k), -math.inf)
-        bias[..., n_k // 2] = 0.0
-    elif case == 'large_biases':  # a per-key bias far above the distance term
-        bias = 40.0 * torch.randn(2, 2, 1, n_k, generator=gen)
-    elif case == 'ragged_mask':
-        bias = torch.zeros(2, 1, 1, n_k)
-        bias[0, ..., n_k // 3:] = -math.inf
-    return q, k, v, scale, bias
-
-
-@pytest.mark.parametrize('case', ['far_points', 'negative_scale', 'zero_scale', 'fully_masked', 'one_live_key',
-                                  'large_biases', 'ragged_mask'])
+@pytest.mark.parametrize('case', HALF_CASES)
 @pytest.mark.parametrize('shape', sorted(HALF_KERNEL_SHAPES))
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16], ids=str)
 def test_16bit_edge_cases(case, shape, dtype):
