@@ -372,19 +372,12 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
   // computed once more with each query's exact maximum subtracted.
   f32x4 acc[kPer][G::kDTiles];
   f32x4 total[kPer];
-  // Weights of block t as packed 16-bit hi / lo pairs (keys 4g + 0,1 and
-  // 4g + 2,3).  16-dim heads run at 64 registers, which the split's two
-  // constant registers would overflow.
+  // Weights of block t as packed 16-bit hi / lo pairs (keys 4g + 0,1 and 4g + 2,3).
   auto weights = [&](const float (&xt)[4], uint32_t* hi, uint32_t* lo) {
     const float w0 = __builtin_amdgcn_exp2f(xt[0]), w1 = __builtin_amdgcn_exp2f(xt[1]);
     const float w2 = __builtin_amdgcn_exp2f(xt[2]), w3 = __builtin_amdgcn_exp2f(xt[3]);
-    if constexpr (kD == 16) {
-      Ops::split2_sub(w0, w1, hi[0], lo[0]);
-      Ops::split2_sub(w2, w3, hi[1], lo[1]);
-    } else {
-      Ops::split2(w0, w1, hi[0], lo[0]);
-      Ops::split2(w2, w3, hi[1], lo[1]);
-    }
+    Ops::split2(w0, w1, hi[0], lo[0]);
+    Ops::split2(w2, w3, hi[1], lo[1]);
   };
   // Logits of key block t for query block j (relative to `shift`, per query column).
   auto logits = [&](int j, int t, float shift, float (&xt)[4]) {
