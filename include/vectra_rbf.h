@@ -59,7 +59,8 @@ enum {
   VECTRA_ERR_BAD_STRUCT = 4,       /* struct_size does not match this build */
   VECTRA_ERR_TOO_LARGE = 5,        /* a size exceeds the kernels' index range */
   VECTRA_ERR_LAUNCH = 6,           /* the HIP launch itself failed          */
-  VECTRA_ERR_BAD_VARIANT = 7       /* forced kernel variant cannot run this problem */
+  VECTRA_ERR_BAD_VARIANT = 7,      /* forced kernel variant cannot run this problem */
+  VECTRA_ERR_BAD_FLAGS = 8         /* flags has bits this build does not know */
 };
 
 /* Kernel variants (for benchmarks and tests; VECTRA_VARIANT_AUTO in production). */
@@ -111,8 +112,21 @@ typedef struct vectra_rbf_args {
   int64_t bias_stride_b, bias_stride_h, bias_stride_n;
 
   int32_t variant;  /* VECTRA_VARIANT_*; 0 picks automatically */
-  int32_t reserved;
+  int32_t flags;    /* VECTRA_FLAG_* bits; 0 by default (other bits are rejected) */
 } vectra_rbf_args;
+
+/*
+ * VECTRA_FLAG_SPLIT_WEIGHTS: the tile kernel keeps every weight as a 16-bit
+ * hi + lo pair (2^-17 of it).  By default, on key axes of 1024 keys or more
+ * with no bias and scale >= 0, it first rounds each weight once to fp16 (2^-11
+ * of it, one product instead of two) and keeps that result where every
+ * query's weight sum is at least 256: its error is at most 2^-11 of the
+ * spread of the values (the bound the reference accepts for fp16,
+ * kernels/tests/test_parity.py:16-23), and in practice ~2^-11 / sqrt(sum) of
+ * it.  Other kernels ignore the flag.  (No counterpart in the reference: its
+ * kernel rounds the weights to the input dtype, spatial_rbf_attention.py:163.)
+ */
+enum { VECTRA_FLAG_SPLIT_WEIGHTS = 1 };
 
 /*
  * Enqueues the fused forward pass on `stream`.

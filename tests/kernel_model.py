@@ -22,6 +22,15 @@ query's own maximum logit subtracted; the tile kernel takes the exact passes
 (a maximum pass, then a shifted pass) for every query of its work item when
 a bias is present, gamma < 0, or any sum falls below the range.
 
+The tile kernel's fast pass (no bias, gamma >= 0, at least FAST_KEYS keys)
+comes first: each weight rounded once to fp16 (to nearest), no split, and the
+values in fp16 (bf16 values converted toward zero).  It stands if every sum
+of the work item is at least FAST_SUM and every value is below 2^16 in
+magnitude; otherwise the item takes the split pass above.
+
+Each query's path is reported as SPLIT (one unshifted split pass), SHIFTED
+(recomputed with its maximum subtracted) or FAST.
+
 Sums here are taken in float64 and rounded once (the matrix cores' order of
 accumulation is not modelled), so the kernels match this model to ~1e-6
 relative, not bit for bit.  tests/test_kernel_model.py bounds the model's
@@ -36,6 +45,9 @@ LOG2E = F32(1.4426950408889634)
 TWO_LOG2E = F32(2.0) * LOG2E
 SUM_RANGE = {'bf16': (F32(2.0 ** -32), F32(2.0 ** 32)), 'fp16': (F32(2.0 ** -3), F32(2.0 ** 15))}
 TILE_ITEM_ROWS = 128  # query rows of one tile-kernel work item (4 waves x 2 blocks x 16)
+FAST_KEYS = 1024      # the tile kernel tries its fast pass from this many keys
+FAST_SUM = F32(256)   # and keeps it if every weight sum of the item is at least this
+SPLIT, SHIFTED, FAST = 0, 1, 2  # per-query paths
 
 
 def to_bf16(x):
@@ -77,6 +89,15 @@ def exp2_32(x):
         return np.exp2(np.asarray(x, np.float64)).astype(F32)
 
 
+def _weighted_fast(x, v16):
+    """(acc, total) of the fast pass: fp16 weights (nearest) against fp16 values."""
+    w = exp2_32(x).astype(np.float16).astype(np.float64)
+    with np.errstate(invalid='ignore', over='ignore'):
+        acc = (w @ v16.astype(np.float64)).astype(F32)
+        total = w.sum(-1).astype(F32)
+    return acc, total
+
+
 def _weighted(x, shift, v, kind):
     """(acc [n, dv], total [n]) of logits x [n, nk] with per-row shifts."""
     w = exp2_32((x - shift[:, None]).astype(F32) if shift is not None else x)
@@ -114,13 +135,13 @@ def _folded_keys(k, gamma, bias):
 def plane(q, k, v, gamma, bias, kind, one_pass=False):
     """rbf_plane_kernel on one plane: q [nq, d], k [nk, d], v [nk, dv] (values
     already in the 16-bit type), gamma, bias [nk] or None.  Returns (out
-    [nq, dv] float32, per-query flags of the shifted recompute)."""
+    [nq, dv] float32, per-query paths: SPLIT or SHIFTED)."""
     q, k, v = (np.asarray(a, F32) for a in (q, k, v))
     coef, c = _folded_keys(k, gamma, bias)
     s = (q.astype(np.float64) @ k.astype(np.float64).T).astype(F32)
     nq = q.shape[0]
     out = np.zeros((nq, v.shape[1]), F32)
-    shifted = np.zeros(nq, bool)
+    path = np.full(nq, SPLIT, np.int8)
     for b0 in range(0, nq, 16):
         rows = slice(b0, min(b0 + 16, nq))
         x0 = fma32(coef, s[rows], c[None, :])
@@ -129,25 +150,37 @@ def plane(q, k, v, gamma, bias, kind, one_pass=False):
             shift = _row_max(x0)
             x = fma32(coef, s[rows], (c[None, :] - shift[:, None]).astype(F32))
             acc, total = _weighted(x, None, v, kind)
-            shifted[rows] = True
+            path[rows] = SHIFTED
         out[rows] = _finish(acc, total)
-    return out, shifted
+    return out, path
 
 
-def tile(q, k, v, gamma, bias, kind, one_pass=False):
+def tile(q, k, v, gamma, bias, kind, one_pass=False, split_weights=False):
     """rbf_tile_kernel on one plane (work items of 128 query rows); same
-    arguments and results as `plane`."""
+    arguments as `plane`, paths SPLIT, SHIFTED or FAST.  `one_pass` models
+    the split pass alone (no fast pass, no recompute); `split_weights` the
+    VECTRA_FLAG_SPLIT_WEIGHTS flag (no fast pass)."""
     q, k, v = (np.asarray(a, F32) for a in (q, k, v))
     coef, c = _folded_keys(k, gamma, bias)
     nq = q.shape[0]
     half_q = (F32(-0.5) * (q.astype(np.float64) ** 2).sum(-1).astype(F32)).astype(F32)
     s = ((q.astype(np.float64) @ k.astype(np.float64).T) + half_q[:, None].astype(np.float64)).astype(F32)
     out = np.zeros((nq, v.shape[1]), F32)
-    shifted = np.zeros(nq, bool)
+    path = np.full(nq, SPLIT, np.int8)
     exact_always = bias is not None or not (coef >= 0)
+    fast = not exact_always and not one_pass and not split_weights and k.shape[0] >= FAST_KEYS
+    if fast:
+        v16 = v if kind == 'fp16' else to_fp16_rtz(v)
+        fits = bool((np.abs(v) < 65536).all())  # False with a NaN
     for r0 in range(0, nq, TILE_ITEM_ROWS):
         rows = slice(r0, min(r0 + TILE_ITEM_ROWS, nq))
         x0 = fma32(coef, s[rows], c[None, :])
+        if fast:
+            acc, total = _weighted_fast(x0, v16)
+            if fits and (total >= FAST_SUM).all():
+                out[rows] = _finish(acc, total)
+                path[rows] = FAST
+                continue
         exact = exact_always and not one_pass
         if not exact:
             acc, total = _weighted(x0, None, v, kind)
@@ -155,25 +188,26 @@ def tile(q, k, v, gamma, bias, kind, one_pass=False):
             exact = not one_pass and not (total >= lo).all()
         if exact:
             acc, total = _weighted(x0, _row_max(x0), v, kind)
-            shifted[rows] = True
+            path[rows] = SHIFTED
         out[rows] = _finish(acc, total)
-    return out, shifted
+    return out, path
 
 
-def run(model, q, k, v, scale, bias, kind, one_pass=False):
+def run(model, q, k, v, scale, bias, kind, one_pass=False, split_weights=False):
     """A model over [B, H, n, d] torch or numpy operands with the operator's
     broadcasting (scale [1|B, 1|H, 1, 1] or a scalar; bias [B, 1|H, 1, nk] or
-    None).  Returns (out [B, H, nq, dv] float32, shifted [B, H, nq])."""
+    None).  Returns (out [B, H, nq, dv] float32, paths [B, H, nq])."""
     q, k, v = (np.asarray(a, F32) for a in (q, k, v))
     batch, heads, nq, _ = q.shape
     sc = np.asarray(scale, F32)
     sc = np.broadcast_to(sc.reshape(sc.shape[:2]) if sc.ndim == 4 else sc.reshape(1, 1), (batch, heads))
     bs = None if bias is None else np.broadcast_to(np.asarray(bias, F32)[:, :, 0, :], (batch, heads, k.shape[2]))
-    fn = plane if model == 'plane' else tile
+    extra = {'split_weights': split_weights} if model == 'tile' else {}
     out = np.zeros((batch, heads, nq, v.shape[-1]), F32)
-    shifted = np.zeros((batch, heads, nq), bool)
+    path = np.zeros((batch, heads, nq), np.int8)
     for b in range(batch):
         for h in range(heads):
-            out[b, h], shifted[b, h] = fn(q[b, h], k[b, h], v[b, h], sc[b, h],
-                                          None if bs is None else bs[b, h], kind, one_pass)
-    return out, shifted
+            fn = plane if model == 'plane' else tile
+            out[b, h], path[b, h] = fn(q[b, h], k[b, h], v[b, h], sc[b, h],
+                                       None if bs is None else bs[b, h], kind, one_pass, **extra)
+    return out, path

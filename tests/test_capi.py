@@ -31,8 +31,8 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_strings():
-    assert capi.abi_version() == (1, 2)
-    for status in range(8):
+    assert capi.abi_version() == (1, 3)
+    for status in range(9):
         assert capi.status_string(status)
     assert capi.status_string(capi.OK) == 'ok'
     assert capi.status_string(99) == 'unknown status'
@@ -175,6 +175,8 @@ def test_forcing_a_variant_that_cannot_run_is_an_error():
         ('q', None, capi.ERR_NULL_ARGUMENT),
         ('scale', None, capi.ERR_NULL_ARGUMENT),
         ('variant', 11, capi.ERR_BAD_VARIANT),
+        ('flags', 2, capi.ERR_BAD_FLAGS),
+        ('flags', -1, capi.ERR_BAD_FLAGS),
     ],
 )
 def test_invalid_arguments_are_rejected_before_any_launch(field, value, status):
@@ -183,6 +185,13 @@ def test_invalid_arguments_are_rejected_before_any_launch(field, value, status):
     assert capi.select_variant(a) == -status
     lib = _native.hip_library()
     assert lib.vectra_rbf_attention_fwd(ctypes.byref(a), None) == status
+
+
+def test_the_split_weights_flag_is_accepted_by_every_variant():
+    for variant in ('auto', 'generic', 'stream'):
+        a = _fake_args(variant=variant)
+        a.flags = capi.FLAG_SPLIT_WEIGHTS
+        assert capi.select_variant(a) > 0, variant
 
 
 def test_empty_problems_are_a_no_op():

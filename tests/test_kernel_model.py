@@ -50,8 +50,8 @@ def test_both_branches_are_taken():
         for case in HALF_CASES:
             for shape in ('plane32', 'tile32'):
                 q, k, v, scale, bias = _case(case, shape, kind)
-                _, shifted = km.run(shape[:-2], q, k, v, scale, bias, kind)
-                seen[(kind, case, shape)] = shifted.mean()
+                _, path = km.run(shape[:-2], q, k, v, scale, bias, kind)
+                seen[(kind, case, shape)] = (path == km.SHIFTED).mean()
     for kind in KINDS:
         # Far points: the weights underflow unshifted (a block is recomputed
         # when any of its 16 queries leaves the range).
@@ -68,7 +68,7 @@ def test_both_branches_are_taken():
         for case in ('negative_scale', 'zero_scale', 'ragged_mask'):
             assert seen[(kind, case, 'tile32')] == 1.0, case
         q, k, v, _, _ = _case('ragged_mask', 'tile32', kind)
-        assert not km.run('tile', q, k, v, torch.tensor(0.01), None, kind)[1].any()
+        assert (km.run('tile', q, k, v, torch.tensor(0.01), None, kind)[1] == km.SPLIT).all()
 
 
 # Cases where one unshifted pass misses the gate: weights that overflow
@@ -158,3 +158,134 @@ def test_dropping_the_clamp_costs_no_more_than_the_expansion_error(kind, norm, g
     d32 = (qn.float() + kn.float() - 2 * q @ k.transpose(-1, -2)).double()
     d64 = ((q.double()[..., :, None, :] - k.double()[..., None, :, :]) ** 2).sum(-1)
     assert (gamma * (d32 - d64).abs() <= bound).all()
+
+
+# The tile kernel's fast pass (fp16 weights, no split) on long key axes.
+
+def _long_keys(seed, kind, n_k=1280, n_q=160, dim=64, gamma=0.03):
+    """A plane like config 4's (q, k ~ 0.5 N(0, 1), v ~ N(0, 1)) with a key
+    axis long enough for the fast pass; 160 queries are two work items."""
+    gen = torch.Generator().manual_seed(seed)
+    q = 0.5 * torch.randn(1, 1, n_q, dim, generator=gen)
+    k = 0.5 * torch.randn(1, 1, n_k, dim, generator=gen)
+    v = torch.randn(1, 1, n_k, dim, generator=gen)
+    dt = KINDS[kind]
+    return q.to(dt).float(), k.to(dt).float(), v.to(dt).float(), torch.tensor(gamma), None
+
+
+def _concentrated(seed, n_live, kind, n_k=1024, n_q=32, dim=64):
+    """Weights held by `n_live` keys (each in (1/2, 1]) against values of +-4,
+    the rest of the keys far away: the fewer live keys, the less the fp16
+    rounding errors of the weights average out."""
+    gen = torch.Generator().manual_seed(seed)
+    q = 0.02 * torch.randn(1, 1, n_q, dim, generator=gen)
+    u = torch.randn(n_k, dim, generator=gen)
+    u = u / u.norm(dim=-1, keepdim=True)
+    dist = torch.full((n_k,), 40.0)
+    dist[:n_live] = 0.69 * torch.rand(n_live, generator=gen)
+    k = (u * dist.sqrt()[:, None])[None, None]
+    v = torch.randn(1, 1, n_k, dim, generator=gen)
+    v[..., :n_live, :] = 4 * torch.sign(torch.randn(n_live, dim, generator=gen))
+    dt = KINDS[kind]
+    return q.to(dt).float(), k.to(dt).float(), v.to(dt).float(), torch.tensor(1.0), None
+
+
+@pytest.mark.parametrize('kind', sorted(KINDS))
+def test_the_fast_pass_runs_where_it_holds(kind):
+    q, k, v, scale, bias = _long_keys(1, kind)
+    assert (km.run('tile', q, k, v, scale, bias, kind)[1] == km.FAST).all()
+    # Shorter key axes, a bias, or gamma < 0 never try it.
+    short = _long_keys(1, kind, n_k=km.FAST_KEYS - 24)
+    assert (km.run('tile', *short, kind)[1] == km.SPLIT).all()
+    assert (km.run('tile', q, k, v, scale, torch.zeros(1, 1, 1, k.shape[2]), kind)[1] == km.SHIFTED).all()
+    assert (km.run('tile', q, k, v, torch.tensor(-0.01), bias, kind)[1] == km.SHIFTED).all()
+    # Weight sums below FAST_SUM (a large gamma) send the item to the split.
+    assert (km.run('tile', q, k, v, torch.tensor(0.3), bias, kind)[1] != km.FAST).all()
+    # Per work item: queries far from the keys in the second item only.
+    far = q.clone()
+    far[..., 128:, :] += 1.5
+    far = far.to(KINDS[kind]).float()
+    path = km.run('tile', far, k, v, scale, bias, kind)[1][0, 0]
+    assert (path[:128] == km.FAST).all() and (path[128:] != km.FAST).all()
+
+
+def test_values_fp16_cannot_hold_send_the_item_to_the_split():
+    q, k, v, scale, bias = _long_keys(2, 'bf16')
+    v[..., 7, 3] = 2.0 ** 17  # a bf16 value beyond fp16's range
+    got, path = km.run('tile', q, k, v, scale, bias, 'bf16')
+    assert (path == km.SPLIT).all()
+    want = oracle.expanded_fp64(q, k, v, scale, bias)
+    np.testing.assert_allclose(got, want, **HALF_TOL)
+
+
+@pytest.mark.parametrize('kind', sorted(KINDS))
+@pytest.mark.parametrize('gamma', [0.005, 0.03, 0.05])
+def test_the_fast_pass_meets_the_gate_on_long_keys(kind, gamma):
+    """Config 4's key axis and range of gamma: the fast pass holds for every
+    query, stays within the reference's fp16 bound (2^-11 of the spread of
+    the values, kernels/tests/test_parity.py:16-23) and within the 1e-3 /
+    1e-4 gate."""
+    q, k, v, scale, bias = _long_keys(int(gamma * 1000), kind, n_k=4096, gamma=gamma)
+    got, path = km.run('tile', q, k, v, scale, bias, kind)
+    assert (path == km.FAST).all()
+    want = oracle.expanded_fp64(q, k, v, scale, bias)
+    vv = v.double().numpy()[0, 0]
+    spread = vv.max(0) - vv.min(0)
+    assert (np.abs(got - want) <= 2.0 ** -11 * spread + 1e-6).all()
+    np.testing.assert_allclose(got, want, **HALF_TOL)
+
+
+def _walk_sigma(q, k, v, gamma):
+    """Per query, the scale of the fp16 weights' random walk: 2^-12 / sqrt(3)
+    (the deviation of a rounding error uniform over half a step of 2^-11)
+    times max |v - out| times sqrt(sum w^2) / sum w, in float64."""
+    qq, kk, vv = (t.double().numpy()[0, 0] for t in (q, k, v))
+    d = ((qq[:, None, :] - kk[None, :, :]) ** 2).sum(-1)
+    w = np.exp(-gamma * d)
+    w = w / w.max(-1, keepdims=True)
+    out = w @ vv / w.sum(-1, keepdims=True)
+    dev = np.abs(vv[None, :, :] - out[:, None, :]).max(1).max(-1)
+    return 2.0 ** -12 / np.sqrt(3) * dev * np.sqrt((w ** 2).sum(-1)) / w.sum(-1)
+
+
+def _bf16_weights(x, v16):
+    """The fast pass with the weights rounded to bf16 (2^-9) instead."""
+    w = km.to_bf16(km.exp2_32(x)).astype(np.float64)
+    return (w @ v16.astype(np.float64)).astype(km.F32), w.sum(-1).astype(km.F32)
+
+
+@pytest.mark.parametrize('kind', sorted(KINDS))
+def test_the_fast_pass_error_is_a_random_walk(kind, monkeypatch):
+    """At the guard's edge (weight sums ~275 over ~380 keys, values +-4) the
+    error of every output stays within 6 deviations of the walk; weights
+    rounded to bf16 (as the reference rounds them for bf16 inputs) go past
+    it.  (Relative to the absolute 1e-4 of the gate, values of +-4 at this
+    sum come to ~1.2e-4: VECTRA_FLAG_SPLIT_WEIGHTS keeps the split.)"""
+    for seed in range(3):
+        q, k, v, scale, bias = _concentrated(seed, 380, kind)
+        got, path = km.run('tile', q, k, v, scale, bias, kind)
+        assert (path == km.FAST).all()
+        want = oracle.expanded_fp64(q, k, v, scale, bias)
+        sigma = _walk_sigma(q, k, v, 1.0)[:, None]
+        assert (np.abs(got - want)[0, 0] <= 6 * sigma).all()
+        monkeypatch.setattr(km, '_weighted_fast', _bf16_weights)
+        coarse, _ = km.run('tile', q, k, v, scale, bias, kind)
+        monkeypatch.undo()
+        assert (np.abs(coarse - want)[0, 0] > 6 * sigma).any()
+
+
+@pytest.mark.parametrize('kind', sorted(KINDS))
+def test_the_weight_sum_guard_is_needed(kind, monkeypatch):
+    """Weights held by a few keys: the model takes the split pass and meets
+    the gate; the fast pass kept regardless would miss it."""
+    for n_live in (4, 16, 64):
+        q, k, v, scale, bias = _concentrated(n_live, n_live, kind)
+        want = oracle.expanded_fp64(q, k, v, scale, bias)
+        got, path = km.run('tile', q, k, v, scale, bias, kind)
+        assert (path == km.SPLIT).all()
+        np.testing.assert_allclose(got, want, **HALF_TOL)
+        monkeypatch.setattr(km, 'FAST_SUM', km.F32(0))
+        forced, path = km.run('tile', q, k, v, scale, bias, kind)
+        monkeypatch.undo()
+        assert (path == km.FAST).all()
+        assert not np.allclose(forced, want, **HALF_TOL), n_live

@@ -21,7 +21,7 @@ import torch
 from oracle import rbf as oracle
 from tests import kernel_model as km
 from tests.half_cases import HALF_CASES, HALF_KERNEL_SHAPES, half_case
-from tests.test_kernel_model import _large_norm_case
+from tests.test_kernel_model import _concentrated, _large_norm_case, _long_keys
 from vectra_amd.kernels import capi
 
 pytestmark = pytest.mark.gpu
@@ -30,9 +30,10 @@ MODEL_TOL = {'rtol': 1e-4, 'atol': 2e-5}
 KINDS = {'bf16': torch.bfloat16, 'fp16': torch.float16}
 
 
-def _kernel(q, k, v, scale, bias, dtype, variant):
+def _kernel(q, k, v, scale, bias, dtype, variant, split_weights=False):
     out = capi.forward(q.to('cuda', dtype), k.to('cuda', dtype), v.to('cuda', dtype), scale.cuda(),
-                       None if bias is None else bias.cuda(), out_dtype=torch.float32, variant=variant)
+                       None if bias is None else bias.cuda(), out_dtype=torch.float32, variant=variant,
+                       split_weights=split_weights)
     torch.cuda.synchronize()
     return out.cpu().numpy()
 
@@ -70,3 +71,33 @@ def test_large_norms_without_the_clamp(kind, norm, gamma):
         print(f'norm={norm} gamma={gamma} kind={kind} variant={variant}: error {err:.3g}, '
               f'reference algorithm in fp32 {ref_err:.3g}', flush=True)
         assert err <= 2 * ref_err + 1e-5
+
+
+def _long_key_cases(kind):
+    """Long key axes through each of the tile kernel's paths: (name, inputs,
+    split_weights flag, number of leading queries on the fast pass)."""
+    q, k, v, scale, bias = _long_keys(1, kind)
+    far = q.clone()
+    far[..., 128:, :] += 1.5
+    far = far.to(KINDS[kind]).float()  # the model takes the inputs the kernel sees
+    yield 'fast', (q, k, v, scale, bias), False, 160
+    yield 'second_item_below_the_guard', (far, k, v, scale, bias), False, 128
+    yield 'large_gamma', (q, k, v, torch.tensor(0.3), bias), False, 0
+    yield 'few_live_keys', _concentrated(16, 16, kind), False, 0
+    yield 'guard_edge', _concentrated(0, 380, kind), False, 32
+    yield 'split_flag', (q, k, v, scale, bias), True, 0
+    if kind == 'bf16':
+        big = v.clone()
+        big[..., 7, 3] = 2.0 ** 17
+        yield 'value_beyond_fp16', (q, k, big, scale, bias), False, 0
+
+
+@pytest.mark.parametrize('kind', sorted(KINDS))
+def test_the_tile_kernel_follows_the_model_on_long_keys(kind):
+    for name, (q, k, v, scale, bias), split, n_fast in _long_key_cases(kind):
+        print(f'long keys: case={name} kind={kind} split_weights={split}', flush=True)
+        want, path = km.run('tile', q, k, v, scale, bias, kind, split_weights=split)
+        fast = (path[0, 0] == km.FAST)
+        assert fast[:n_fast].all() and not fast[n_fast:].any(), name
+        got = _kernel(q, k, v, scale, bias, KINDS[kind], 'tile', split_weights=split)
+        np.testing.assert_allclose(got, want, err_msg=name, **MODEL_TOL)

@@ -46,9 +46,9 @@ def _variants(q, k, v, scale, bias):
     return found
 
 
-def run(q, k, v, scale, bias=None, variant='auto', out_dtype=torch.float32):
+def run(q, k, v, scale, bias=None, variant='auto', out_dtype=torch.float32, split_weights=False):
     out = capi.forward(_cuda(q), _cuda(k), _cuda(v), _cuda(scale), _cuda(bias),
-                       out_dtype=out_dtype, variant=variant)
+                       out_dtype=out_dtype, variant=variant, split_weights=split_weights)
     torch.cuda.synchronize()
     return out.cpu()
 
@@ -113,9 +113,10 @@ def test_long_key_rows_against_the_expansion():
     assert config.head_dim == 64
     want = oracle.expanded_fp64(q, k, v, scale)
     for variant in _variants(q, k, v, scale, None):
-        print(f'long_key slice variant={variant}', flush=True)
-        got = run(q, k, v, scale, None, variant).double().numpy()
-        np.testing.assert_allclose(got, want, **HALF_TOL)
+        for split in (False, True):  # the tile kernel's fp16-weight pass, then the split kept
+            print(f'long_key slice variant={variant} split_weights={split}', flush=True)
+            got = run(q, k, v, scale, None, variant, split_weights=split).double().numpy()
+            np.testing.assert_allclose(got, want, **HALF_TOL)
 
 
 def test_operator_output_is_the_rounded_fp32_result():
@@ -177,9 +178,19 @@ def test_full_long_key_size_properties():
     q, k, v, scale, bias = inputs.args()
     assert bias is None
     base = capi.forward(q, k, v, scale, None, out_dtype=torch.float32)
-    # Scaling V by a power of two scales every output exactly.
+    # Scaling V by a power of two scales every output exactly with the split
+    # weights.  The fp16-weight pass (the default here) converts bf16 values
+    # below 2^-14 toward zero in fp16's subnormal steps of 2^-24, so there
+    # the doubled values agree to that step (plus an ulp of the output).
+    split = capi.forward(q, k, v, scale, None, out_dtype=torch.float32, split_weights=True)
+    doubled = capi.forward(q, k, v * 2, scale, None, out_dtype=torch.float32, split_weights=True)
+    assert torch.equal(doubled, split * 2)
     doubled = capi.forward(q, k, v * 2, scale, None, out_dtype=torch.float32)
-    assert torch.equal(doubled, base * 2)
+    torch.testing.assert_close(doubled, base * 2, rtol=2.0 ** -22, atol=2.0 ** -22)
+    # The two agree within the gate: the fp16 weights' rounding errors add up
+    # like a random walk of ~2^-12 / sqrt(3 sum) of the values' spread (sums of
+    # 400-3500 weights here: ~2e-5 at most over the 67M outputs).
+    torch.testing.assert_close(base, split, **HALF_TOL)
     # Planes and query rows are independent: a sub-batch of planes and a
     # permutation of the query rows reproduce their outputs.
     part = capi.forward(q[3:5, 7:9], k[3:5, 7:9], v[3:5, 7:9], scale[:, 7:9], None, out_dtype=torch.float32)

@@ -43,7 +43,7 @@ using vectra::make_fast_div;
 using vectra::Problem;
 
 constexpr int kAbiMajor = 1;
-constexpr int kAbiMinor = 2;
+constexpr int kAbiMinor = 3;
 
 bool is_io_dtype(int32_t d) { return d == VECTRA_F32 || d == VECTRA_F16 || d == VECTRA_BF16; }
 bool is_any_dtype(int32_t d) { return is_io_dtype(d) || d == VECTRA_F64; }
@@ -91,6 +91,7 @@ int validate(const vectra_rbf_args* a) {
     return VECTRA_ERR_BAD_SHAPE;
   if (a->variant < VECTRA_VARIANT_AUTO || a->variant > VECTRA_VARIANT_TILE)
     return VECTRA_ERR_BAD_VARIANT;
+  if ((a->flags & ~VECTRA_FLAG_SPLIT_WEIGHTS) != 0) return VECTRA_ERR_BAD_FLAGS;
   // Each size below 2^31 keeps every product of two or three of them in int64.
   constexpr int64_t kMaxDim = 0x7fffffffLL;
   if (a->batch > kMaxDim || a->heads > kMaxDim || a->n_q > kMaxDim || a->n_k > kMaxDim ||
@@ -137,6 +138,7 @@ Problem make_problem(const vectra_rbf_args* a) {
   p.sbh = a->bias_stride_h;
   p.sbn = a->bias_stride_n;
   p.total_rows = a->batch * a->heads * a->n_q;
+  p.flags = a->flags;
   make_fast_div(a->n_q > 0 ? a->n_q : 1, &p.nq_mul, &p.nq_shift);
   make_fast_div(a->heads > 0 ? a->heads : 1, &p.h_mul, &p.h_shift);
   return p;
@@ -274,6 +276,7 @@ const char* vectra_rbf_status_string(int status) {
     case VECTRA_ERR_TOO_LARGE: return "problem exceeds the kernel grid limits";
     case VECTRA_ERR_LAUNCH: return "HIP kernel launch failed";
     case VECTRA_ERR_BAD_VARIANT: return "the requested kernel variant cannot run this problem";
+    case VECTRA_ERR_BAD_FLAGS: return "unknown bits in flags";
     default: return "unknown status";
   }
 }

@@ -30,6 +30,7 @@ struct Problem {
   int64_t total_rows;  // B * H * Nq
   int32_t grid_waves;  // waves launched by persistent kernels (<= total_rows)
   int32_t compute_units;  // of the device the launch runs on
+  int32_t flags;          // VECTRA_FLAG_* bits
   uint32_t nq_mul, nq_shift;  // FastDiv of Nq (see fast_div)
   uint32_t h_mul, h_shift;    // FastDiv of H
 };

@@ -33,6 +33,19 @@
 // the expansion negative, -d and the reference's max(d, 0) = 0 are both
 // within the expansion's rounding error of the true distance.
 //
+// Fast pass (one pass, long key axes): with at least kFastKeys keys, the
+// single pass first runs with each weight rounded once to fp16 (to nearest,
+// 2^-11 of the weight) and fp16 values (bf16 values converted as they are
+// staged, exactly where they lie in fp16's normal range), one product
+// instead of the hi and lo pair and no split.  Its error is at most 2^-11 of
+// the spread of the values, the bound the reference accepts for fp16
+// (kernels/tests/test_parity.py:16-23); rounding errors of independent
+// weights add up like a random walk, and a weight sum T >= kFastSum (each
+// weight is at most 1, so at least T keys carry the sum) keeps that walk
+// below 2^-11 / sqrt(T) of the spread.  If any query of the item ends with
+// T < kFastSum, or a bf16 value is too large for fp16, the item takes the
+// split pass as above.
+//
 // Scheduling: persistent workgroups take items in a fixed order.  With a
 // grid and an item count that are multiples of the 8 XCDs (workgroups are
 // dispatched round-robin over them), the items are ordered so that every
@@ -89,8 +102,17 @@ struct TileStage {
   uint32_t bias_misalign;
 };
 
-// Pass kinds of one item.
-enum TilePass : int { kPassSum = 0, kPassMax = 1, kPassShifted = 2 };
+// Pass kinds of one item, as template arguments of the pass code.
+enum TilePass : int { kPassSum = 0, kPassMax = 1, kPassShifted = 2, kPassFast = 3 };
+template <int kKind>
+struct PassKind {
+  static constexpr int value = kKind;
+};
+
+// The fast pass: tried for key axes of at least kFastKeys keys, kept if every
+// query's weight sum is at least kFastSum (see the header comment).
+constexpr int32_t kFastKeys = 1024;
+constexpr float kFastSum = 256.f;
 
 // Three waves per SIMD (at most 168 VGPRs) measured fastest for head dims
 // up to 64; 128-dim heads keep two.
@@ -115,6 +137,7 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
 
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ int32_t exact_flag[2];
+  __shared__ int32_t split_flag[2];  // the fast pass did not hold
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -181,9 +204,16 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
     }
   };
 
+  // The largest |v| a fast pass converted from bf16 to fp16 (this thread).
+  float v_big = 0.f;
+
   // Writes a staged tile into LDS buffer `buf`: K and V rows, and per key
-  // c_j = log2(e) bias_j - coef |k_j|^2 / 2 (-inf past Nk).
-  auto publish = [&](const Stage& st, int32_t tile, int buf, float coef) {
+  // c_j = log2(e) bias_j - coef |k_j|^2 / 2 (-inf past Nk).  A fast pass
+  // stores bf16 values as fp16 (round toward zero: exact for bf16 values in
+  // fp16's normal range, within 2^-24 below it; values of 2^16 or more,
+  // which fp16 cannot hold, are caught through v_big).
+  auto publish = [&](const Stage& st, int32_t tile, int buf, float coef, auto kind_c) {
+    constexpr bool kToF16 = decltype(kind_c)::value == kPassFast && kBf16;
     const int32_t j0 = tile * kKeys;
     T* kl = reinterpret_cast<T*>(lds + buf * G::kBufBytes);
     T* vl = reinterpret_cast<T*>(lds + buf * G::kBufBytes + G::kKBytes);
@@ -197,8 +227,17 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
         *reinterpret_cast<uint4*>(kl + key * G::kKStride + d0) = st.k[s];
         // Rows past Nk are zeroed in V: their weight is 0, and 0 times a
         // non-finite copy would not be.
-        *reinterpret_cast<uint4*>(vl + key * G::kVStride + d0) =
-            j0 + key < n_k ? st.v[s] : make_uint4(0, 0, 0, 0);
+        uint4 vw = st.v[s];
+        if constexpr (kToF16) {
+          uint32_t* w = reinterpret_cast<uint32_t*>(&vw);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float f0 = __uint_as_float(w[e] << 16), f1 = __uint_as_float(w[e] & 0xffff0000u);
+            v_big = fmaxf(v_big, fmaxf(fabsf(f0), fabsf(f1)));
+            w[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f0, f1));
+          }
+        }
+        *reinterpret_cast<uint4*>(vl + key * G::kVStride + d0) = j0 + key < n_k ? vw : make_uint4(0, 0, 0, 0);
         // |k|^2 over the chunks of the row (kChunks adjacent lanes).
         const float sq = reduce_low<kChunks>(dot_chunk<T>(st.k[s], st.k[s], 0.f), OpSum());
         if (slot % kChunks == 0) {
@@ -226,7 +265,8 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
   f32x4 total[kCB];
 
   // Reduces tile `buf` for the wave's 32 queries.
-  auto compute = [&](int buf, float coef, int kind) {
+  auto compute = [&](int buf, float coef, auto kind_c) {
+    constexpr int kind = decltype(kind_c)::value;
     const T* kl = reinterpret_cast<const T*>(lds + buf * G::kBufBytes);
     const T* vl = reinterpret_cast<const T*>(lds + buf * G::kBufBytes + G::kKBytes);
     const float* cl = reinterpret_cast<const float*>(lds + buf * G::kBufBytes + G::kKBytes + G::kVBytes);
@@ -256,12 +296,47 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
           x[cb][hb][3] = fmaf(coef, s[cb][hb][3], c.w);
         }
       }
-      if (kind == kPassMax) {
+      if constexpr (kind == kPassMax) {
 #pragma unroll
         for (int cb = 0; cb < kCB; ++cb)
 #pragma unroll
           for (int hb = 0; hb < 2; ++hb)
             row_max[cb] = fmaxf(row_max[cb], fmaxf(fmaxf(x[cb][hb][0], x[cb][hb][1]), fmaxf(x[cb][hb][2], x[cb][hb][3])));
+        continue;
+      }
+      if constexpr (kind == kPassFast) {
+        // One fp16 weight per score (round to nearest) against fp16 values.
+        using H = MfmaOps<_Float16>;
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        typename H::Qk pw[kCB];
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb) {
+          uint32_t wp[4];
+#pragma unroll
+          for (int hb = 0; hb < 2; ++hb) {
+            float w[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) w[r] = __builtin_amdgcn_exp2f(x[cb][hb][r]);
+            wp[2 * hb] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{w[0], w[1]}, h2));
+            wp[2 * hb + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{w[2], w[3]}, h2));
+          }
+          pw[cb] = __builtin_bit_cast(typename H::Qk, make_uint4(wp[0], wp[1], wp[2], wp[3]));
+        }
+#pragma unroll
+        for (int u = 0; u < kDTiles; ++u) {
+          // The A operand as in the split pass below.
+          const T* va = vl + (32 * kp + 4 * grp + col / 4) * G::kVStride + 16 * u + 4 * (col % 4);
+          const uint2 a0 = lds_read_tr16(va);
+          const uint2 a1 = lds_read_tr16(va + 16 * G::kVStride);
+          const auto a = __builtin_bit_cast(typename H::Qk, make_uint4(a0.x, a0.y, a1.x, a1.y));
+#pragma unroll
+          for (int cb = 0; cb < kCB; ++cb) acc[cb][u] = H::qk(a, pw[cb], acc[cb][u]);
+        }
+        const uint32_t one_h = MfmaOps<_Float16>::kOnePair;
+        const auto ones_h = __builtin_bit_cast(typename H::Qk, make_uint4(one_h, one_h, one_h, one_h));
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb) total[cb] = H::qk(ones_h, pw[cb], total[cb]);
+        __builtin_amdgcn_sched_barrier(0);
         continue;
       }
       Qk p_hi[kCB], p_lo[kCB];
@@ -312,8 +387,8 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
   // One pass of an item over every key tile (double-buffered, one barrier
   // per tile).  Every wave of the workgroup runs it.
   Stage st;
-  auto run_pass = [&](const Coords& c, float coef, int kind) {
-    if (kind != kPassMax) {
+  auto run_pass = [&](const Coords& c, float coef, auto kind_c) {
+    if constexpr (decltype(kind_c)::value != kPassMax) {
 #pragma unroll
       for (int cb = 0; cb < kCB; ++cb) {
 #pragma unroll
@@ -322,12 +397,12 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
       }
     }
     issue(st, c, 0);
-    publish(st, 0, 0, coef);
+    publish(st, 0, 0, coef, kind_c);
     __syncthreads();
     if (tiles > 1) issue(st, c, 1);
     for (int32_t t = 0; t < tiles; ++t) {
-      compute(t & 1, coef, kind);
-      if (t + 1 < tiles) publish(st, t + 1, (t + 1) & 1, coef);
+      compute(t & 1, coef, kind_c);
+      if (t + 1 < tiles) publish(st, t + 1, (t + 1) & 1, coef, kind_c);
       __syncthreads();
       if (t + 2 < tiles) issue(st, c, t + 2);
     }
@@ -336,7 +411,10 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
   int32_t parity = 0;
   for (int32_t slot = static_cast<int32_t>(blockIdx.x); slot < items; slot += grid, parity ^= 1) {
     const Coords c = coords(item_of(slot));
-    if (tid == 0) exact_flag[parity] = 0;  // read after the first barrier of this item
+    if (tid == 0) {  // read after the first barrier of this item
+      exact_flag[parity] = 0;
+      split_flag[parity] = 0;
+    }
     const float coef = 2.f * kLog2e * load_any(p.scale, c.b * p.ssb + c.h * p.ssh, p.scale_dtype);
     // Query rows of this wave: item rows (wave * kCB + cb) * 16 + col (rows
     // past Nq read row Nq - 1 and are not stored).
@@ -357,8 +435,21 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
     }
     // The single pass needs x <= 0: no bias and gamma >= 0.
     bool exact = has_bias || !(coef >= 0.f);
-    if (!exact) {
-      run_pass(c, coef, kPassSum);
+    bool split = true;
+    if (!exact && n_k >= kFastKeys && !(p.flags & VECTRA_FLAG_SPLIT_WEIGHTS)) {
+      v_big = 0.f;
+      run_pass(c, coef, PassKind<kPassFast>{});
+      // A weight sum below kFastSum (or NaN), or a value fp16 cannot hold,
+      // anywhere in the workgroup sends the item to the split pass.
+      bool redo = !(v_big < 65536.f);
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) redo = redo || !(total[cb][0] >= kFastSum);
+      if (__builtin_amdgcn_ballot_w64(redo) && lane == 0) split_flag[parity] = 1;
+      __syncthreads();
+      split = split_flag[parity] != 0;
+    }
+    if (!exact && split) {
+      run_pass(c, coef, PassKind<kPassSum>{});
       // A weight sum below the accurate range (or NaN) anywhere in the
       // workgroup sends the item to the exact passes.
       bool low = false;
@@ -371,13 +462,13 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
     if (exact) {
 #pragma unroll
       for (int cb = 0; cb < kCB; ++cb) row_max[cb] = -INFINITY;
-      run_pass(c, coef, kPassMax);
+      run_pass(c, coef, PassKind<kPassMax>{});
 #pragma unroll
       for (int cb = 0; cb < kCB; ++cb) {
         const float m = allreduce_bit32(allreduce_bit16(row_max[cb], OpMax()), OpMax());
         row_max[cb] = m == -INFINITY ? 0.f : m;  // every key masked: the row ends as NaN
       }
-      run_pass(c, coef, kPassShifted);
+      run_pass(c, coef, PassKind<kPassShifted>{});
     }
 
     // Store: every row of the ones product holds the query's weight sum; a

@@ -25,6 +25,8 @@ ERR_BAD_STRUCT = 4
 ERR_TOO_LARGE = 5
 ERR_LAUNCH = 6
 ERR_BAD_VARIANT = 7
+ERR_BAD_FLAGS = 8
+FLAG_SPLIT_WEIGHTS = 1  # VECTRA_FLAG_SPLIT_WEIGHTS
 
 # Kernel variants.
 VARIANTS = {'auto': 0, 'generic': 1, 'stream': 2, 'mfma': 3, 'plane': 4, 'tile': 5}
@@ -73,7 +75,7 @@ class RbfArgs(ctypes.Structure):
         ('bias_stride_h', ctypes.c_int64),
         ('bias_stride_n', ctypes.c_int64),
         ('variant', ctypes.c_int32),
-        ('reserved', ctypes.c_int32),
+        ('flags', ctypes.c_int32),
     ]
 
 
@@ -114,7 +116,7 @@ def broadcast_operands(q, k, scale, key_bias):
     return scale4, bias4
 
 
-def make_args(q, k, v, out, scale4, bias4, variant: str = 'auto') -> RbfArgs:
+def make_args(q, k, v, out, scale4, bias4, variant: str = 'auto', flags: int = 0) -> RbfArgs:
     """Fills struct vectra_rbf_args from tensors (pointers, sizes, strides)."""
     a = RbfArgs()
     a.struct_size = ctypes.sizeof(RbfArgs)
@@ -137,6 +139,7 @@ def make_args(q, k, v, out, scale4, bias4, variant: str = 'auto') -> RbfArgs:
         a.bias_stride_b, a.bias_stride_h = bias4.stride(0), bias4.stride(1)
         a.bias_stride_n = bias4.stride(3)
     a.variant = VARIANTS[variant]
+    a.flags = flags
     return a
 
 
@@ -164,6 +167,7 @@ def forward(
     out_dtype=None,
     out=None,
     variant: str = 'auto',
+    split_weights: bool = False,
     stream=None,
 ):
     """Runs the fused kernel through the C ABI; returns `out`.
@@ -172,7 +176,9 @@ def forward(
       q, k, v, scale, key_bias: as torch.ops.vectra.rbf_attention (GPU tensors).
       out_dtype: output dtype (default v.dtype); ignored when `out` is given.
       out: optional preallocated [B, H, Nq, Dv] output (any strides).
-      variant: 'auto', 'generic', 'stream' or 'mfma'.
+      variant: 'auto', 'generic', 'stream', 'mfma', 'plane' or 'tile'.
+      split_weights: VECTRA_FLAG_SPLIT_WEIGHTS (the tile kernel keeps hi + lo
+        weights on long key axes instead of its fp16-weight pass).
       stream: hipStream_t as an int (default: torch's current stream).
     """
     if not q.is_cuda:
@@ -186,7 +192,8 @@ def forward(
             dtype=out_dtype or v.dtype,
             device=q.device,
         )
-    launch(make_args(q, k, v, out, scale4, bias4, variant), stream)
+    flags = FLAG_SPLIT_WEIGHTS if split_weights else 0
+    launch(make_args(q, k, v, out, scale4, bias4, variant, flags), stream)
     return out
 
 
