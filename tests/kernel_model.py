@@ -24,9 +24,9 @@ a bias is present, gamma < 0, or any sum falls below the range.
 
 The tile kernel's fast pass (no bias, gamma >= 0, at least FAST_KEYS keys)
 comes first: each weight rounded once to fp16 (to nearest), no split, and the
-values in fp16 (bf16 values converted toward zero).  It stands if every sum
-of the work item is at least FAST_SUM and every value is below 2^16 in
-magnitude; otherwise the item takes the split pass above.
+values in fp16 (bf16 values converted to nearest, 2^16 and beyond to inf).
+It stands if every sum of the work item is at least FAST_SUM and every
+accumulator is finite; otherwise the item takes the split pass above.
 
 Each query's path is reported as SPLIT (one unshifted split pass), SHIFTED
 (recomputed with its maximum subtracted) or FAST.
@@ -170,14 +170,14 @@ def tile(q, k, v, gamma, bias, kind, one_pass=False, split_weights=False):
     exact_always = bias is not None or not (coef >= 0)
     fast = not exact_always and not one_pass and not split_weights and k.shape[0] >= FAST_KEYS
     if fast:
-        v16 = v if kind == 'fp16' else to_fp16_rtz(v)
-        fits = bool((np.abs(v) < 65536).all())  # False with a NaN
+        with np.errstate(over='ignore'):
+            v16 = v.astype(np.float16).astype(F32)  # exact for fp16 inputs
     for r0 in range(0, nq, TILE_ITEM_ROWS):
         rows = slice(r0, min(r0 + TILE_ITEM_ROWS, nq))
         x0 = fma32(coef, s[rows], c[None, :])
         if fast:
             acc, total = _weighted_fast(x0, v16)
-            if fits and (total >= FAST_SUM).all():
+            if np.isfinite(acc).all() and (total >= FAST_SUM).all():
                 out[rows] = _finish(acc, total)
                 path[rows] = FAST
                 continue

@@ -198,6 +198,18 @@ __device__ __forceinline__ void unpack<_Float16>(const uint4& r, float* f) {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// A buffer resource over `bytes` bytes from `base`: loads past the end read
+// as zeros.  Word 3 is the gfx9 data-format field of a raw buffer.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+// Cache policy of the streaming loads: non-temporal.
+constexpr int kNt = 2;
+__device__ __forceinline__ uint4 load16_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNt);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ __forceinline__ uint4 load16(const void* p) {
   return *static_cast<const uint4*>(p);
 }

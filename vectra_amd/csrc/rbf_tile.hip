@@ -26,6 +26,11 @@ bool tile_supports(const Problem& p, int in_dtype, int out_dtype) {
       ((p.Nk - 1) * p.sv[2] + p.Dv) * 2 > kMax32)
     return false;
   if (p.bias != nullptr && (p.Nk - 1) * p.sbn * (p.bias_dtype == VECTRA_F32 ? 4 : 2) + 4 > kMax32) return false;
+  // K and V tiles are loaded whole: the offsets of rows up to the last
+  // tile's end (64 keys, 32 for 128-dim heads) stay 32-bit.
+  const int64_t keys_padded = (p.Nk + 63) / 64 * 64;
+  if (((keys_padded - 1) * p.sk[2] + p.D) * 2 > kMax32 || ((keys_padded - 1) * p.sv[2] + p.Dv) * 2 > kMax32)
+    return false;
   // Output offsets inside a plane are 32-bit byte counts: the last element of
   // the plane's output view must lie within 4 GiB of the plane's first.
   const int64_t out_size = out_dtype == VECTRA_F32 ? 4 : 2;

@@ -35,16 +35,17 @@
 //
 // Fast pass (one pass, long key axes): with at least kFastKeys keys, the
 // single pass first runs with each weight rounded once to fp16 (to nearest,
-// 2^-11 of the weight) and fp16 values (bf16 values converted as they are
-// staged, exactly where they lie in fp16's normal range), one product
-// instead of the hi and lo pair and no split.  Its error is at most 2^-11 of
-// the spread of the values, the bound the reference accepts for fp16
-// (kernels/tests/test_parity.py:16-23); rounding errors of independent
+// 2^-11 of the weight) and fp16 values (bf16 values converted to nearest as
+// they are staged: exact in fp16's normal range, within 2^-25 below it), one
+// product instead of the hi and lo pair and no split.  Its error is at most
+// 2^-11 of the spread of the values, the bound the reference accepts for
+// fp16 (kernels/tests/test_parity.py:16-23); rounding errors of independent
 // weights add up like a random walk, and a weight sum T >= kFastSum (each
 // weight is at most 1, so at least T keys carry the sum) keeps that walk
 // below 2^-11 / sqrt(T) of the spread.  If any query of the item ends with
-// T < kFastSum, or a bf16 value is too large for fp16, the item takes the
-// split pass as above.
+// T < kFastSum or a non-finite accumulator (a bf16 value of 2^16 or more
+// becomes inf in fp16, and inf times any weight, 0 included, is not finite),
+// the item takes the split pass as above.
 //
 // Scheduling: persistent workgroups take items in a fixed order.  With a
 // grid and an item count that are multiples of the 8 XCDs (workgroups are
@@ -176,21 +177,27 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
     return c;
   };
 
-  // Issues the loads of tile `tile` of the plane of `c` into `st`.  Rows past
-  // Nk read row Nk - 1 (in bounds) and are masked when published.
+  // Byte offsets of a thread's first K and V chunk within a tile; slot s
+  // adds s * kThreads / kChunks rows.
+  static_assert(G::kFull && kThreads % kChunks == 0, "whole rows per slot");
+  const uint32_t k_lane = static_cast<uint32_t>(tid / kChunks) * k_row_bytes + static_cast<uint32_t>(tid % kChunks) * 16u;
+  const uint32_t v_lane = static_cast<uint32_t>(tid / kChunks) * v_row_bytes + static_cast<uint32_t>(tid % kChunks) * 16u;
+
+  // Issues the loads of tile `tile` of the plane of `c` into `st`: buffer
+  // loads over the plane's rows, so rows past Nk read zeros (or, where rows
+  // overlap, bytes of the plane's own rows; no offset wraps, which the
+  // launch checks) and are masked when published.
   auto issue = [&](Stage& st, const Coords& c, int32_t tile) {
     const char* kp = static_cast<const char*>(p.k) + (c.b * p.sk[0] + c.h * p.sk[1]) * 2;
     const char* vp = static_cast<const char*>(p.v) + (c.b * p.sv[0] + c.h * p.sv[1]) * 2;
+    const auto k_rsrc = plane_rsrc(kp, static_cast<uint32_t>(n_k - 1) * k_row_bytes + kD * 2);
+    const auto v_rsrc = plane_rsrc(vp, static_cast<uint32_t>(n_k - 1) * v_row_bytes + kD * 2);
     const int32_t j0 = tile * kKeys;
 #pragma unroll
     for (int s = 0; s < G::kSlots; ++s) {
-      const int slot = tid + s * kThreads;
-      if (G::kFull || slot < kKeys * kChunks) {
-        const uint32_t row = static_cast<uint32_t>(min(j0 + slot / kChunks, n_k - 1));
-        const uint32_t chunk_off = static_cast<uint32_t>(slot % kChunks) * 16u;
-        st.k[s] = load16_stream(kp + row * k_row_bytes + chunk_off);
-        st.v[s] = load16_stream(vp + row * v_row_bytes + chunk_off);
-      }
+      const uint32_t row0 = static_cast<uint32_t>(j0 + s * (kThreads / kChunks));
+      st.k[s] = load16_buf(k_rsrc, k_lane + row0 * k_row_bytes);
+      st.v[s] = load16_buf(v_rsrc, v_lane + row0 * v_row_bytes);
     }
     if (has_bias) {
       const char* bp = static_cast<const char*>(p.bias) + (c.b * p.sbb + c.h * p.sbh) * bias_esize;
@@ -204,14 +211,9 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
     }
   };
 
-  // The largest |v| a fast pass converted from bf16 to fp16 (this thread).
-  float v_big = 0.f;
-
   // Writes a staged tile into LDS buffer `buf`: K and V rows, and per key
   // c_j = log2(e) bias_j - coef |k_j|^2 / 2 (-inf past Nk).  A fast pass
-  // stores bf16 values as fp16 (round toward zero: exact for bf16 values in
-  // fp16's normal range, within 2^-24 below it; values of 2^16 or more,
-  // which fp16 cannot hold, are caught through v_big).
+  // stores bf16 values as fp16 (to nearest).
   auto publish = [&](const Stage& st, int32_t tile, int buf, float coef, auto kind_c) {
     constexpr bool kToF16 = decltype(kind_c)::value == kPassFast && kBf16;
     const int32_t j0 = tile * kKeys;
@@ -229,15 +231,16 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
         // non-finite copy would not be.
         uint4 vw = st.v[s];
         if constexpr (kToF16) {
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
           uint32_t* w = reinterpret_cast<uint32_t*>(&vw);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float f0 = __uint_as_float(w[e] << 16), f1 = __uint_as_float(w[e] & 0xffff0000u);
-            v_big = fmaxf(v_big, fmaxf(fabsf(f0), fabsf(f1)));
-            w[e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f0, f1));
+            w[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{f0, f1}, h2));
           }
         }
-        *reinterpret_cast<uint4*>(vl + key * G::kVStride + d0) = j0 + key < n_k ? vw : make_uint4(0, 0, 0, 0);
+        if (j0 + kKeys > n_k && j0 + key >= n_k) vw = make_uint4(0, 0, 0, 0);  // the last tile only
+        *reinterpret_cast<uint4*>(vl + key * G::kVStride + d0) = vw;
         // |k|^2 over the chunks of the row (kChunks adjacent lanes).
         const float sq = reduce_low<kChunks>(dot_chunk<T>(st.k[s], st.k[s], 0.f), OpSum());
         if (slot % kChunks == 0) {
@@ -437,13 +440,20 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
     bool exact = has_bias || !(coef >= 0.f);
     bool split = true;
     if (!exact && n_k >= kFastKeys && !(p.flags & VECTRA_FLAG_SPLIT_WEIGHTS)) {
-      v_big = 0.f;
       run_pass(c, coef, PassKind<kPassFast>{});
-      // A weight sum below kFastSum (or NaN), or a value fp16 cannot hold,
-      // anywhere in the workgroup sends the item to the split pass.
-      bool redo = !(v_big < 65536.f);
+      // A weight sum below kFastSum (or NaN), or a non-finite accumulator (a
+      // value fp16 cannot hold), anywhere in the workgroup sends the item to
+      // the split pass.  A finite accumulator is at most Nk * 2^16 < 2^47 in
+      // size, so their sum is finite exactly when every one of them is.
+      float acc_sum = 0.f;
+      bool redo = false;
 #pragma unroll
-      for (int cb = 0; cb < kCB; ++cb) redo = redo || !(total[cb][0] >= kFastSum);
+      for (int cb = 0; cb < kCB; ++cb) {
+        redo = redo || !(total[cb][0] >= kFastSum);
+#pragma unroll
+        for (int u = 0; u < kDTiles; ++u) acc_sum += (acc[cb][u][0] + acc[cb][u][1]) + (acc[cb][u][2] + acc[cb][u][3]);
+      }
+      redo = redo || !__builtin_isfinite(acc_sum);
       if (__builtin_amdgcn_ballot_w64(redo) && lane == 0) split_flag[parity] = 1;
       __syncthreads();
       split = split_flag[parity] != 0;
