@@ -308,6 +308,32 @@ def test_non_finite_values_in_masked_rows_propagate(shape, dtype):
         np.testing.assert_allclose(got, want, equal_nan=True, err_msg=variant, **tol)
 
 
+@pytest.mark.parametrize('shape', [(65, 65, 32), (24, 70, 16), (33, 128, 16), (40, 64, 32)], ids=str)
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16], ids=str)
+def test_skipped_masked_blocks_are_bit_exact(shape, dtype):
+    """The plane kernel skips the products of 16-key blocks whose keys are
+    all masked (with finite K and V rows).  A finite bias of -1e30 masks the
+    same keys (their weights are exactly 0) but keeps their blocks, so the
+    two give bit-identical outputs."""
+    n_q, n_k, dim = shape
+    gen = torch.Generator().manual_seed(12)
+    q = torch.randn(4, 2, n_q, dim, generator=gen).to(dtype)
+    k = torch.randn(4, 2, n_k, dim, generator=gen).to(dtype)
+    v = torch.randn(4, 2, n_k, dim, generator=gen).to(dtype)
+    counts = torch.tensor([1, n_k, 17, n_k // 2])  # live keys per batch entry
+    masked = (torch.arange(n_k)[None, :] >= counts[:, None])[:, None, None, :]
+    skip_bias = torch.zeros(4, 1, 1, n_k).masked_fill(masked, -math.inf)
+    keep_bias = torch.zeros(4, 1, 1, n_k).masked_fill(masked, -1e30)
+    scale = torch.tensor(0.04)
+    for out_dtype in (dtype, torch.float32):
+        print(f'shape={shape} dtype={dtype} out={out_dtype}', flush=True)
+        skipped = run(q, k, v, scale, skip_bias, 'plane', out_dtype=out_dtype)
+        kept = run(q, k, v, scale, keep_bias, 'plane', out_dtype=out_dtype)
+        assert torch.equal(skipped, kept)
+    want = oracle.expanded_fp64(q, k, v, scale, skip_bias)
+    np.testing.assert_allclose(skipped.double().numpy(), want, **HALF_TOL)  # the fp32 output
+
+
 def test_far_points_do_not_underflow():
     gen = torch.Generator().manual_seed(6)
     q = torch.randn(2, 2, 10, 32, generator=gen) * 20

@@ -185,6 +185,10 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
   __shared__ __align__(16) T vt_lds[kD * G::kVStride];
   __shared__ __align__(16) char k_lds[kKeys * G::kKStride];
   __shared__ __align__(16) float c_lds[kKeys];  // folded key values
+  // Per key: whether it can contribute (not masked with a finite K row), and
+  // per key and 16-byte chunk of V, whether the chunk holds an inf or NaN.
+  __shared__ __align__(4) uint8_t k_live[kKeys];
+  __shared__ __align__(4) uint8_t v_bad[kKeys * kChunks];
 
   const int tid = static_cast<int>(threadIdx.x);
   const int nthreads = static_cast<int>(blockDim.x);
@@ -302,7 +306,11 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
               : p.bias_dtype == VECTRA_BF16 ? __uint_as_float(bias_raw << 16)
                                             : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bias_raw)));
         }
-        c_lds[row] = row < n_k ? fmaf(half_coef, sq, x * kLog2e) : -INFINITY;
+        const float c = row < n_k ? fmaf(half_coef, sq, x * kLog2e) : -INFINITY;
+        c_lds[row] = c;
+        // A key masked by its bias (or past Nk) whose K row is finite gets
+        // weight exactly 0 from every finite query.
+        k_live[row] = !(row >= n_k || (c == -INFINITY && __builtin_isfinite(sq)));
       }
     }
   };
@@ -311,6 +319,16 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
   auto put_v = [&](int i, uint4 r0, uint4 r1) {
     const int row = 2 * (i / kChunks);
     const int d0 = (i % kChunks) * 8;
+    // An all-ones exponent in either 16-bit half: (w & exp) + low carries
+    // into that half's top bit, and into nothing else.
+    constexpr uint32_t kExp = kBf16 ? 0x7f807f80u : 0x7c007c00u;
+    constexpr uint32_t kLow = kBf16 ? 0x00800080u : 0x04000400u;
+    auto bad = [&](uint4 r) {
+      const uint32_t m = ((r.x & kExp) + kLow) | ((r.y & kExp) + kLow) | ((r.z & kExp) + kLow) | ((r.w & kExp) + kLow);
+      return static_cast<uint8_t>((m & 0x80008000u) != 0);
+    };
+    v_bad[row * kChunks + i % kChunks] = bad(r0);
+    v_bad[(row + 1) * kChunks + i % kChunks] = bad(r1);
     const uint32_t w0[4] = {r0.x, r0.y, r0.z, r0.w};
     const uint32_t w1[4] = {r1.x, r1.y, r1.z, r1.w};
     T* dst = vt_lds + d0 * G::kVStride + G::vt_pos(row);
@@ -339,6 +357,28 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
   static_assert(kRowsPerWave * kChunks == kWave, "pieces of whole rows per wave");
 
   __syncthreads();  // K, the folded key values and V^T in place
+
+  // 16-key blocks that can contribute: a block whose every key is masked
+  // with finite K and V rows adds exact zeros to every sum (bit for bit), so
+  // its products are skipped.  Bit t of live_blocks is block t (uniform).
+  auto key_live = [&](int j) -> bool {
+    if (j >= kKeys) return false;
+    uint32_t bad;
+    if constexpr (kChunks == 4) {
+      bad = *reinterpret_cast<const uint32_t*>(v_bad + 4 * j);
+    } else {
+      static_assert(kChunks == 2, "16- or 32-dim heads");
+      bad = *reinterpret_cast<const uint16_t*>(v_bad + 2 * j);
+    }
+    return k_live[j] != 0 || bad != 0;
+  };
+  const uint64_t live_lo = __builtin_amdgcn_ballot_w64(key_live(lane));
+  const uint64_t live_hi = kKeys > 64 ? __builtin_amdgcn_ballot_w64(key_live(lane + 64)) : 0;
+  uint32_t live_blocks = 0;
+#pragma unroll
+  for (int t = 0; t < kNB; ++t)
+    if (((t < 4 ? live_lo >> (16 * t) : live_hi >> (16 * (t - 4))) & 0xffffu) != 0) live_blocks |= 1u << t;
+  live_blocks = __builtin_amdgcn_readfirstlane(live_blocks);
 
   // Key block t's operand of the first product (read from LDS where it is
   // used rather than held across the pass, which would cost a wave slot).
@@ -389,6 +429,7 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
     }
 #pragma unroll
     for (int pp = 0; pp < kNB / 2; ++pp) {
+      if (((live_blocks >> (2 * pp)) & 3u) == 0) continue;
       Qk p_hi[n], p_lo[n];
 #pragma unroll
       for (int j = 0; j < n; ++j) {
@@ -419,6 +460,7 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
     }
     if constexpr (kNB % 2 == 1) {
       constexpr int t = kNB - 1;
+      if (((live_blocks >> t) & 1u) == 0) return;
       Pv p_hi[n], p_lo[n];
 #pragma unroll
       for (int j = 0; j < n; ++j) {
@@ -450,6 +492,7 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
     float rmax = -INFINITY;
 #pragma unroll
     for (int t = 0; t < kNB; ++t) {
+      if (((live_blocks >> t) & 1u) == 0) continue;
       float xt[4];
       logits(j, t, 0.f, xt);
       rmax = fmaxf(rmax, fmaxf(fmaxf(xt[0], xt[1]), fmaxf(xt[2], xt[3])));
