@@ -309,12 +309,12 @@ def test_non_finite_values_in_masked_rows_propagate(shape, dtype):
 
 
 @pytest.mark.parametrize('shape', [(65, 65, 32), (24, 70, 16), (33, 128, 16), (40, 64, 32)], ids=str)
-@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16, torch.float32], ids=str)
 def test_skipped_masked_blocks_are_bit_exact(shape, dtype):
-    """The plane kernel skips the products of 16-key blocks whose keys are
-    all masked (with finite K and V rows).  A finite bias of -1e30 masks the
-    same keys (their weights are exactly 0) but keeps their blocks, so the
-    two give bit-identical outputs."""
+    """The plane kernels skip the products of 16-key blocks (and the fp32
+    kernel its tail keys) whose keys are all masked with finite K and V
+    rows.  A finite bias of -1e30 masks the same keys (their weights are
+    exactly 0) but keeps their blocks, so the two give bit-identical outputs."""
     n_q, n_k, dim = shape
     gen = torch.Generator().manual_seed(12)
     q = torch.randn(4, 2, n_q, dim, generator=gen).to(dtype)
@@ -331,7 +331,8 @@ def test_skipped_masked_blocks_are_bit_exact(shape, dtype):
         kept = run(q, k, v, scale, keep_bias, 'plane', out_dtype=out_dtype)
         assert torch.equal(skipped, kept)
     want = oracle.expanded_fp64(q, k, v, scale, skip_bias)
-    np.testing.assert_allclose(skipped.double().numpy(), want, **HALF_TOL)  # the fp32 output
+    tol = FP32_TOL if dtype == torch.float32 else HALF_TOL
+    np.testing.assert_allclose(skipped.double().numpy(), want, **tol)  # the fp32 output
 
 
 def test_far_points_do_not_underflow():

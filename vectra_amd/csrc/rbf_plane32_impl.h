@@ -23,7 +23,10 @@
 //    cross-lane steps at the end, not a product;
 //  * key blocks past Nk are skipped, and up to 4 keys past the last whole
 //    block (65 keys: one) go through the VALU instead of a block of products
-//    that would be mostly padding.
+//    that would be mostly padding;
+//  * as in the 16-bit kernel, a key block (or tail key) whose every key is
+//    masked with finite K and V rows adds exact zeros to every sum and is
+//    skipped, bit for bit.
 // Weights are used unshifted while a query's sum stays in [2^-100, 2^32]
 // (value products overflow only for |v| > 2^96, and subnormal weights lie
 // under 2^-20 of the sum); outside
@@ -80,6 +83,10 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
   __shared__ __align__(16) float vt_lds[kD * G::kVtStride];
   __shared__ __align__(16) char k_lds[kKeys * G::kKStride];
   __shared__ __align__(16) float c_lds[kKeys];  // folded key values
+  // Per key: whether it can contribute (not masked with a finite K row), and
+  // per key and 16-byte chunk of V, whether the chunk holds an inf or NaN.
+  __shared__ __align__(8) uint8_t k_live[kKeys];
+  __shared__ __align__(8) uint8_t v_bad[kKeys * kChunks];
 
   const int tid = static_cast<int>(threadIdx.x);
   const int nthreads = static_cast<int>(blockDim.x);
@@ -191,6 +198,10 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
       vt_lds[(d0 + 1) * G::kVtStride + row] = __uint_as_float(vpiece.y);
       vt_lds[(d0 + 2) * G::kVtStride + row] = __uint_as_float(vpiece.z);
       vt_lds[(d0 + 3) * G::kVtStride + row] = __uint_as_float(vpiece.w);
+      // An all-ones exponent: (w & exp) + low carries into the sign bit.
+      const uint32_t m = ((vpiece.x & 0x7f800000u) + 0x00800000u) | ((vpiece.y & 0x7f800000u) + 0x00800000u) |
+                         ((vpiece.z & 0x7f800000u) + 0x00800000u) | ((vpiece.w & 0x7f800000u) + 0x00800000u);
+      v_bad[row * kChunks + static_cast<int>(chunk_off) / 16] = static_cast<uint8_t>(m >> 31);
       if (chunk_off == 0) {
         float x = 0.f;
         if (has_bias) {
@@ -198,7 +209,11 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
               : p.bias_dtype == VECTRA_BF16 ? __uint_as_float(bias_raw << 16)
                                             : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bias_raw)));
         }
-        c_lds[row] = row < n_k ? fmaf(half_coef, sq, x * kLog2e) : -INFINITY;
+        const float c = row < n_k ? fmaf(half_coef, sq, x * kLog2e) : -INFINITY;
+        c_lds[row] = c;
+        // A key masked by its bias (or past Nk) whose K row is finite gets
+        // weight exactly 0 from every finite query.
+        k_live[row] = !(row >= n_k || (c == -INFINITY && __builtin_isfinite(sq)));
       }
     }
   };
@@ -212,6 +227,29 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
     put(base, k_piece(base / kChunks), v_piece(base / kChunks), bias_of(base / kChunks));
 
   __syncthreads();  // K, the folded key values and V^T in place
+
+  // Keys that can contribute (bit j of live_lo / live_hi) and 16-key blocks
+  // holding one (bit t of live_blocks), uniform over the wave.
+  auto key_live = [&](int j) -> bool {
+    if (j >= kKeys) return false;
+    uint32_t bad;
+    if constexpr (kChunks == 8) {
+      const uint2 r = *reinterpret_cast<const uint2*>(v_bad + 8 * j);
+      bad = r.x | r.y;
+    } else {
+      static_assert(kChunks == 4, "16- or 32-dim heads");
+      bad = *reinterpret_cast<const uint32_t*>(v_bad + 4 * j);
+    }
+    return k_live[j] != 0 || bad != 0;
+  };
+  const uint64_t live_lo = __builtin_amdgcn_ballot_w64(key_live(lane));
+  const uint64_t live_hi = kKeys > 64 ? __builtin_amdgcn_ballot_w64(key_live(lane + 64)) : 0;
+  uint32_t live_blocks = 0;
+#pragma unroll
+  for (int t = 0; t < kNB; ++t)
+    if (((t < 4 ? live_lo >> (16 * t) : live_hi >> (16 * (t - 4))) & 0xffffu) != 0) live_blocks |= 1u << t;
+  live_blocks = __builtin_amdgcn_readfirstlane(live_blocks);
+  auto key_is_live = [&](int kt) { return ((kt < 64 ? live_lo >> kt : live_hi >> (kt - 64)) & 1u) != 0; };
 
   const char* const k_op = k_lds + col * G::kKStride + grp * kSteps * 4;
   f32x4 acc[kPer][G::kDTiles];
@@ -304,9 +342,10 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
     }
 #pragma unroll
     for (int t = 0; t < kNB; ++t)
-      if (t < mfma_blocks) block(n_tag, t, shift);
+      if (t < mfma_blocks && ((live_blocks >> t) & 1u) != 0) block(n_tag, t, shift);
     if (valu_tail)
-      for (int kt = 16 * whole; kt < n_k; ++kt) tail_key(n_tag, kt, shift);
+      for (int kt = 16 * whole; kt < n_k; ++kt)
+        if (key_is_live(kt)) tail_key(n_tag, kt, shift);
     // A query's sum: its lane's keys, then the 4 lanes of its column.
 #pragma unroll
     for (int j = 0; j < kPer; ++j) total[j] = allreduce_bit32(allreduce_bit16(total[j], OpSum()), OpSum());
@@ -315,10 +354,11 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
   auto row_max = [&](int j) __attribute__((always_inline)) {
     float rmax = -INFINITY;
     if (valu_tail)
-      for (int kt = 16 * whole; kt < n_k; ++kt) rmax = fmaxf(rmax, fmaf(coef, tail_score(j, kt), c_lds[kt]));
+      for (int kt = 16 * whole; kt < n_k; ++kt)
+        if (key_is_live(kt)) rmax = fmaxf(rmax, fmaf(coef, tail_score(j, kt), c_lds[kt]));
 #pragma unroll
     for (int t = 0; t < kNB; ++t) {
-      if (t >= mfma_blocks) continue;
+      if (t >= mfma_blocks || ((live_blocks >> t) & 1u) == 0) continue;
       float kf[kSteps];
 #pragma unroll
       for (int c = 0; c < kSteps / 4; ++c) {
