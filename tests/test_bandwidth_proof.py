@@ -25,9 +25,15 @@ def _write(path, header, rows):
     return str(path)
 
 
-def _stats(path, kernels):
-    header = ['Name', 'Calls', 'TotalDurationNs', 'AverageNs', 'Percentage', 'MinNs', 'MaxNs', 'StdDev']
-    return _write(path, header, [[n, c, t, t / c, 0, 0, 0, 0] for n, c, t in kernels])
+def _trace(path, dispatches):
+    """A --kernel-trace CSV of (name, duration_ns) dispatches in launch order."""
+    header = ['Kind', 'Agent_Id', 'Queue_Id', 'Stream_Id', 'Thread_Id', 'Dispatch_Id', 'Kernel_Id', 'Kernel_Name',
+              'Correlation_Id', 'Start_Timestamp', 'End_Timestamp']
+    rows, t = [], 1_000
+    for i, (name, ns) in enumerate(dispatches, 1):
+        rows.append(['KERNEL_DISPATCH', 1, 1, 0, 1, i, 1, name, i, t, t + ns])
+        t += ns + 500
+    return _write(path, header, rows)
 
 
 def _counters(path, counter, dispatches):
@@ -67,19 +73,25 @@ def test_gate_fails_on_bytes_at_any_batch_and_on_a_missing_utilisation_batch():
     assert not bandwidth_proof.evaluate(edge)
 
 
-def test_region_is_aggregated_over_every_dispatch_but_the_runtime_blits(tmp_path):
-    # Two calls of a two-kernel region plus input copies the runtime made.
-    stats = _stats(tmp_path / 'stats.csv', [('kernel_a', 2, 60_000), ('kernel_b', 2, 20_000), (BLIT, 4, 9_999)])
+def test_region_is_aggregated_over_the_measured_calls_but_not_the_runtime_blits(tmp_path):
+    # A warm-up call and two measured calls of a two-kernel region, plus input
+    # copies the runtime made; the warm-up call is slower and reads more.
+    trace = _trace(tmp_path / 'trace.csv', [
+        (BLIT, 9_999), ('kernel_a', 90_000), ('kernel_b', 50_000), (BLIT, 9_999),
+        ('kernel_a', 30_000), ('kernel_b', 10_000), ('kernel_a', 30_000), ('kernel_b', 10_000),
+    ])
     kib = 1024.0
     fetch = _counters(tmp_path / 'fetch.csv', 'FETCH_SIZE', [
-        (BLIT, 512 * kib), ('kernel_a', 12_288 * kib), ('kernel_b', 4_096 * kib),
+        (BLIT, 512 * kib), ('kernel_a', 99_999 * kib), ('kernel_b', 99_999 * kib),
+        ('kernel_a', 12_288 * kib), ('kernel_b', 4_096 * kib),
         ('kernel_a', 12_288 * kib), ('kernel_b', 4_096 * kib),
     ])
     write = _counters(tmp_path / 'write.csv', 'WRITE_SIZE', [
-        (BLIT, 777 * kib), ('kernel_a', 0.0), ('kernel_b', 1_024 * kib),
+        (BLIT, 777 * kib), ('kernel_a', 5.0), ('kernel_b', 5.0),
+        ('kernel_a', 0.0), ('kernel_b', 1_024 * kib),
         ('kernel_a', 0.0), ('kernel_b', 1_024 * kib),
     ])
-    got = bandwidth_proof.region_counters(stats, fetch, write, calls=2, batch=8,
+    got = bandwidth_proof.region_counters(trace, fetch, write, calls=3, warmup=1, batch=8,
                                           scales={'fetch_scale': 2.0, 'write_scale': 1.0})
     read = 2.0 * (12_288 + 4_096) * kib * 1024
     written = 1_024 * kib * 1024
@@ -88,6 +100,9 @@ def test_region_is_aggregated_over_every_dispatch_but_the_runtime_blits(tmp_path
     assert got['dram_bytes'] == read + written
     assert got['dram_bytes_per_query'] == (read + written) / 8
     assert got['kernel_ns'] == 40_000
+    # A dispatch count that does not divide into the calls is an error.
+    with pytest.raises(ValueError):
+        bandwidth_proof.measured_dispatches([1.0] * 5, calls=2, warmup=1)
     # Bytes over summed time: the time-weighted mean of the kernels' rates.
     want_pct = 100 * (read + written) / 40e-6 / roofline.MI355X.hbm_bytes_per_s
     assert got['dram_throughput_pct'] == pytest.approx(want_pct)

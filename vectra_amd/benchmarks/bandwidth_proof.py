@@ -20,9 +20,13 @@ size, `vectra_amd.benchmarks.copy_calibration`).  Per call of the region:
 The default workload is the serving shape (B=1024, H=8, Lq=1, Lk=64, D=32,
 bf16); `--config bandwidth` is the reference's own (H=4, Lq=Lk=65, fp16).
 Each run makes 5 warm-up calls (one per rotating input set, 5 x the
-working set: above the 256 MB Infinity Cache at B=1024) and `--reps` more;
-counters are divided by that number of calls.  It then checks the gates the
-reference reads from its serving SLO:
+working set: above the 256 MB Infinity Cache at B=1024) and `--reps` more.
+The warm-up calls stay outside the measured region, as the reference's
+harness keeps its warm-up outside the profiled NVTX range
+(kernels/benchmarks/bandwidth.py:60-77): times (per dispatch, from the kernel
+trace) and counters are summed over the dispatches of the `--reps` calls
+after them and divided by `--reps`.  It then checks the gates the reference
+reads from its serving SLO:
 
 * fused / eager DRAM bytes <= 0.60 at every batch;
 * fused DRAM throughput >= 65 % of peak at the batch whose working set
@@ -83,32 +87,45 @@ def evaluate(measured: dict, slo: dict = SLO) -> list[str]:
     return failures
 
 
-def region_counter(path: str) -> float:
-    """A counter summed over every dispatch of a run (runtime copy blits excluded)."""
-    total = 0.0
+def measured_dispatches(values: list[float], calls: int, warmup: int) -> list[float]:
+    """The per-dispatch values of the calls after the first `warmup` (every
+    call of the region launches the same number of kernels)."""
+    if calls <= warmup or len(values) % calls:
+        raise ValueError(f'{len(values)} dispatches do not divide into {calls} calls')
+    return values[warmup * (len(values) // calls):]
+
+
+def region_durations_ns(path: str) -> list[float]:
+    """Each dispatch's duration from a `--kernel-trace` CSV, in launch order
+    (runtime copy blits excluded)."""
+    with open(path, encoding='utf-8') as f:
+        rows = [r for r in csv.DictReader(f) if RUNTIME_BLIT not in r['Kernel_Name']]
+    rows.sort(key=lambda r: int(r['Start_Timestamp']))
+    return [float(int(r['End_Timestamp']) - int(r['Start_Timestamp'])) for r in rows]
+
+
+def region_counter_values(path: str) -> list[float]:
+    """A counter per dispatch, in dispatch order (runtime copy blits excluded;
+    rows of one dispatch summed)."""
+    per: dict[int, float] = {}
     with open(path, encoding='utf-8') as f:
         for r in csv.DictReader(f):
             if RUNTIME_BLIT not in r['Kernel_Name']:
-                total += float(r['Counter_Value'])
-    return total
+                key = int(r['Dispatch_Id'])
+                per[key] = per.get(key, 0.0) + float(r['Counter_Value'])
+    return [per[k] for k in sorted(per)]
 
 
-def region_kernel_ns(path: str) -> float:
-    """Total kernel time of a `--kernel-trace --stats` run (copy blits excluded)."""
-    total = 0.0
-    with open(path, encoding='utf-8') as f:
-        for r in csv.DictReader(f):
-            if RUNTIME_BLIT not in r['Name']:
-                total += float(r['TotalDurationNs'])
-    return total
-
-
-def region_counters(stats_csv: str, fetch_csv: str, write_csv: str, calls: int, batch: int,
+def region_counters(trace_csv: str, fetch_csv: str, write_csv: str, calls: int, warmup: int, batch: int,
                     scales: dict) -> dict:
-    """Per-call bytes, time and throughput of a region from its three runs."""
-    read = region_counter(fetch_csv) * 1024.0 * scales['fetch_scale'] / calls
-    write = region_counter(write_csv) * 1024.0 * scales['write_scale'] / calls
-    kernel_ns = region_kernel_ns(stats_csv) / calls
+    """Per-call bytes, time and throughput of a region from its three runs,
+    over the calls after the first `warmup`."""
+    measured = calls - warmup
+    read = sum(measured_dispatches(region_counter_values(fetch_csv), calls, warmup)) * 1024.0 * scales[
+        'fetch_scale'] / measured
+    write = sum(measured_dispatches(region_counter_values(write_csv), calls, warmup)) * 1024.0 * scales[
+        'write_scale'] / measured
+    kernel_ns = sum(measured_dispatches(region_durations_ns(trace_csv), calls, warmup)) / measured
     dram_bytes = read + write
     return {
         'dram_bytes': dram_bytes,
@@ -150,11 +167,11 @@ def measure(config_name: str, batch: int, impl: str, work: str, scales: dict, re
     stats = _rocprof(['--kernel-trace', '--stats'], work, f'{name}_trace', program, 180)
     fetch = _rocprof(['--pmc', 'FETCH_SIZE'], work, f'{name}_fetch', program, 120)
     write = _rocprof(['--pmc', 'WRITE_SIZE'], work, f'{name}_write', program, 120)
-    calls = 5 + reps  # eager_gpu: one warm-up call per input set (5), then --reps
-    return region_counters(os.path.join(stats, f'{name}_trace_kernel_stats.csv'),
+    warmup = 5  # eager_gpu: one warm-up call per input set (5), then --reps
+    return region_counters(os.path.join(stats, f'{name}_trace_kernel_trace.csv'),
                            os.path.join(fetch, f'{name}_fetch_counter_collection.csv'),
                            os.path.join(write, f'{name}_write_counter_collection.csv'),
-                           calls, batch, scales)
+                           warmup + reps, warmup, batch, scales)
 
 
 def main(argv=None) -> int:
