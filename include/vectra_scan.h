@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VECTRA_SCAN_ABI_VERSION 1
+#define VECTRA_SCAN_ABI_VERSION 2
 
 /* Entries of a PQ sub-space's codebook (kPqCentroids,
  * include/vectra/index/simd_distance.h). */
@@ -134,6 +134,46 @@ typedef struct vectra_pq_adc_args {
 } vectra_pq_adc_args;
 
 int vectra_scan_pq_adc(const vectra_pq_adc_args* args, hipStream_t stream);
+
+/* Largest k of vectra_scan_top_k (SearchLimits::max_top_k,
+ * include/vectra/service/search_handler.h:28) and the node of an empty
+ * result slot. */
+#define VECTRA_SCAN_MAX_K 1024
+#define VECTRA_SCAN_NO_NODE 0xFFFFFFFFu
+
+/*
+ * Exhaustive k-nearest search: for every query q, the k candidates nearest
+ * by L2SquaredDistance, as ShardIndex::ExhaustiveSearch returns them
+ * (shard_index.cc:236-264): candidates are the rows ids[0 .. num_ids) (ids
+ * not below num_rows are skipped, :245; duplicates are kept), or every row
+ * when ids is NULL; at most k are kept (PushBounded, :111-120) and they are
+ * ordered by CloserFirst (include/vectra/index/search_scratch.h: distance
+ * ascending, ties by node id ascending).  Result r of query q is
+ * distances[q * out_stride + r] and nodes[q * out_stride + r] (the row
+ * index); slots past the number of candidates hold +inf and
+ * VECTRA_SCAN_NO_NODE.  Distances are bit-identical to vectra_scan_rows'
+ * (NaN distances, which CloserFirst cannot order, rank after every number,
+ * ties by node, and come out as the quiet NaN 0x7fc00000).  k is
+ * 1 .. VECTRA_SCAN_MAX_K; num_rows is below VECTRA_SCAN_NO_NODE.  With
+ * dimension 0 every distance is 0 and `queries` and `rows` may be NULL.
+ */
+typedef struct vectra_scan_top_k_args {
+  int32_t dimension;         /* >= 0 floats per vector */
+  int32_t k;                 /* 1 .. VECTRA_SCAN_MAX_K */
+  const float* queries;      /* [num_queries][query_stride] */
+  int64_t num_queries;
+  int64_t query_stride;      /* >= dimension */
+  const float* rows;         /* [num_rows][row_stride] */
+  int64_t num_rows;
+  int64_t row_stride;        /* >= dimension */
+  const uint32_t* ids;       /* [num_ids] candidate rows, or NULL for every row */
+  int64_t num_ids;
+  float* distances;          /* [num_queries][out_stride] */
+  uint32_t* nodes;           /* [num_queries][out_stride] */
+  int64_t out_stride;        /* >= k */
+} vectra_scan_top_k_args;
+
+int vectra_scan_top_k(const vectra_scan_top_k_args* args, hipStream_t stream);
 
 const char* vectra_scan_status_string(int status);
 int vectra_scan_abi_version(void);

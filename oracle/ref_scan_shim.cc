@@ -4,12 +4,14 @@
 // pq_codec.cc, read in place under /root/reference) into
 // oracle/_ref/libref_scan.so.  Test infrastructure only: the product never
 // loads it.
+#include <algorithm>
 #include <cstdint>
 #include <optional>
 #include <string>
 #include <vector>
 
 #include "vectra/index/pq_codec.h"
+#include "vectra/index/search_scratch.h"
 #include "vectra/index/simd_distance.h"
 
 namespace vi = vectra::index;
@@ -52,6 +54,24 @@ int ref_pq_distance_table(int dim, int subspaces, const float* codebooks, const 
   if (!pq.has_value()) return -1;
   pq->ComputeDistanceTable(query, table);
   return 0;
+}
+
+// The k nearest of candidates (distance[i], node[i]) under the reference's
+// own comparator, CloserFirst (search_scratch.h: distance ascending, ties by
+// node id), the order ExhaustiveSearch returns (shard_index.cc:264).  Writes
+// min(k, n) results and returns that count.  Finite distances only: the
+// comparator is not a strict weak order over NaN.
+int64_t ref_nearest(const float* distance, const uint32_t* node, int64_t n, int64_t k, float* out_distance,
+                    uint32_t* out_node) {
+  std::vector<vi::Neighbor> all(static_cast<size_t>(n));
+  for (int64_t i = 0; i < n; ++i) all[static_cast<size_t>(i)] = {distance[i], node[i]};
+  const int64_t m = std::min(k, n);
+  std::partial_sort(all.begin(), all.begin() + m, all.end(), vi::CloserFirst());
+  for (int64_t i = 0; i < m; ++i) {
+    out_distance[i] = all[static_cast<size_t>(i)].distance;
+    out_node[i] = all[static_cast<size_t>(i)].node;
+  }
+  return m;
 }
 
 }  // extern "C"

@@ -26,6 +26,14 @@ numpy rounds every float32 operation to nearest-even and never fuses a
 multiply into an add, which is what the reference's ISO C++ build does
 (-std=c++20: GCC contracts no expressions in ISO mode).
 
+* ShardIndex::ExhaustiveSearch's selection (shard_index.cc:236-264): the k
+  nearest candidates by L2SquaredDistance, kept by PushBounded (:111-120) in
+  a bounded heap ordered by CloserFirst (search_scratch.h: distance
+  ascending, ties by node id), then sorted by it; candidate ids not below
+  the row count are skipped (:245).  `nearest` restates it as a stable sort
+  on (distance, node); NaN distances, which CloserFirst cannot order, are
+  ranked after every number here, ties by node.
+
 Pins (tests/test_scan_oracle.py): bit-for-bit against the reference sources
 compiled by oracle/Makefile into oracle/_ref (where /root/reference exists),
 the reference's own known-answer tests (simd_parity_test.cc:29-66), a float64
@@ -140,3 +148,29 @@ def pq_distance_table(query, codebooks, subspaces):
     for s in range(subspaces):
         table[s * PQ_CENTROIDS:(s + 1) * PQ_CENTROIDS] = l2_squared(query[s * dsub:(s + 1) * dsub], books[s])
     return table
+
+
+NO_NODE = 0xFFFFFFFF  # node of a result slot past the candidates' count
+
+
+def nearest(queries, rows, k, ids=None):
+    """ExhaustiveSearch's results for each query: (distances [q, k] float32,
+    nodes [q, k] uint32), nearest first by (distance, node); slots past the
+    number of candidates hold +inf and NO_NODE.  Candidate ids >= len(rows)
+    are skipped; duplicate ids are kept, as the reference keeps them."""
+    queries = np.asarray(queries, dtype=np.float32)
+    rows = np.asarray(rows, dtype=np.float32)
+    nodes = np.arange(rows.shape[0], dtype=np.int64) if ids is None else np.asarray(ids, dtype=np.int64)
+    nodes = nodes[nodes < rows.shape[0]]
+    dist = distances(queries, rows, 'l2', nodes)
+    out_d = np.full((queries.shape[0], k), np.inf, dtype=np.float32)
+    out_n = np.full((queries.shape[0], k), NO_NODE, dtype=np.uint32)
+    m = min(k, nodes.shape[0])
+    for q in range(queries.shape[0]):
+        d = dist[q]
+        nan = np.isnan(d)
+        # Keys (nan, distance, node): numbers before NaN, then by node.
+        order = np.lexsort((nodes, np.where(nan, 0, d), nan))[:m]
+        out_d[q, :m] = d[order]
+        out_n[q, :m] = nodes[order]
+    return out_d, out_n

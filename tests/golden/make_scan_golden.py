@@ -1,5 +1,6 @@
 """Writes tests/golden/scan_golden.npz: inputs and the reference engine's own
-outputs for its distance functions.
+outputs for its distance functions and for the selection of
+ShardIndex::ExhaustiveSearch (the k nearest under CloserFirst).
 
 The outputs come from the reference sources themselves (engine/src/index/
 simd_distance.cc and pq_codec.cc under /root/reference), compiled by
@@ -23,6 +24,9 @@ ROW_DIMS = (0, 1, 2, 7, 15, 16, 17, 31, 32, 33, 63, 64, 100, 127, 128, 129, 255,
 ADC_SUBSPACES = (1, 2, 3, 4, 5, 8, 16, 17, 32, 64)
 TABLE_SHAPES = ((128, 16), (96, 32), (40, 8), (18, 1), (64, 2))
 ROWS = 24
+# (rows, dimension, k, with candidate ids)
+NEAREST_CASES = ((200, 32, 50, False), (300, 17, 30, True), (40, 128, 100, False), (25, 0, 10, False),
+                 (120, 64, 120, True))
 
 
 def _p(a):
@@ -61,6 +65,35 @@ def main():
         arrays[f'books_{dim}_{m}'] = books
         arrays[f'tquery_{dim}_{m}'] = query
         arrays[f'table_{dim}_{m}'] = table
+    # The k nearest (CloserFirst, search_scratch.h) among candidates: ids with
+    # duplicates and ids past the row count (ExhaustiveSearch skips those,
+    # shard_index.cc:245), rows repeated so that distances tie, and k above
+    # the candidate count.  Drawn after everything above, so those arrays
+    # are unchanged.
+    for case, (n, dim, k, with_ids) in enumerate(NEAREST_CASES):
+        rows = rng.standard_normal((n, dim)).astype(np.float32)
+        rows[n // 2:n // 2 + n // 10] = rows[:n // 10]  # exact copies: equal distances
+        query = rng.standard_normal(dim).astype(np.float32)
+        if with_ids:
+            ids = rng.integers(0, n + n // 4, size=n, dtype=np.uint32)  # some past the row count
+            ids[: n // 8] = ids[n // 8: 2 * (n // 8)]  # duplicated candidates
+        else:
+            ids = np.arange(n, dtype=np.uint32)
+        cand = ids[ids < n]
+        dist = np.zeros(n, np.float32)
+        lib.ref_scan_rows(0, _p(query), _p(rows), ctypes.c_int64(n), ctypes.c_int64(max(dim, 1)), dim, _p(dist))
+        cand_dist = np.ascontiguousarray(dist[cand.astype(np.int64)])
+        out_d = np.zeros(k, np.float32)
+        out_n = np.zeros(k, np.uint32)
+        lib.ref_nearest.restype = ctypes.c_int64
+        m = lib.ref_nearest(_p(cand_dist), _p(cand), ctypes.c_int64(cand.shape[0]), ctypes.c_int64(k), _p(out_d),
+                            _p(out_n))
+        arrays[f'near_rows_{case}'] = rows
+        arrays[f'near_query_{case}'] = query
+        arrays[f'near_ids_{case}'] = ids if with_ids else np.zeros(0, np.uint32)
+        arrays[f'near_k_{case}'] = np.array(k)
+        arrays[f'near_dist_{case}'] = out_d[:m]
+        arrays[f'near_node_{case}'] = out_n[:m]
     np.savez_compressed(OUT, **arrays)
     print('wrote', OUT, os.path.getsize(OUT), 'bytes')
 

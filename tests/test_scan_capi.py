@@ -27,7 +27,7 @@ def _declared_functions() -> set[str]:
 def test_library_exports_every_declared_symbol():
     declared = _declared_functions()
     assert declared == {'vectra_scan_rows', 'vectra_pq_distance_tables', 'vectra_scan_pq_adc',
-                        'vectra_scan_status_string', 'vectra_scan_abi_version'}
+                        'vectra_scan_top_k', 'vectra_scan_status_string', 'vectra_scan_abi_version'}
     lib = ctypes.CDLL(_native.SCAN_LIBRARY)
     for name in declared:
         assert hasattr(lib, name), name
@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _native.scan_library()
-    assert lib.vectra_scan_abi_version() == 1
+    assert lib.vectra_scan_abi_version() == 2
     assert lib.vectra_scan_status_string(0) == b'ok'
     assert lib.vectra_scan_status_string(1) == b'invalid argument'
     assert lib.vectra_scan_status_string(99) == b'unknown status'
@@ -45,7 +45,7 @@ def test_abi_version_and_status_strings():
 def test_struct_layouts_match_the_header(tmp_path):
     # offsetof / sizeof of the three argument structs from the header itself.
     structs = {'vectra_scan_args': scan._ScanArgs, 'vectra_pq_table_args': scan._PqTableArgs,
-               'vectra_pq_adc_args': scan._PqAdcArgs}
+               'vectra_pq_adc_args': scan._PqAdcArgs, 'vectra_scan_top_k_args': scan._TopKArgs}
     lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "vectra_scan.h"', 'int main(void) {']
     for cname, cls in structs.items():
         lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')
@@ -149,6 +149,36 @@ def _adc_args(**over):
 ])
 def test_adc_arguments(over, status):
     assert _native.scan_library().vectra_scan_pq_adc(ctypes.byref(_adc_args(**over)), None) == status
+
+
+def _top_k_args(**over):
+    fields = dict(dimension=8, k=10, queries=FAKE, num_queries=2, query_stride=8, rows=FAKE, num_rows=100,
+                  row_stride=8, ids=None, num_ids=0, distances=FAKE, nodes=FAKE, out_stride=10)
+    fields.update(over)
+    return scan._TopKArgs(**fields)
+
+
+@pytest.mark.parametrize('over,status', [
+    (dict(k=0), INVALID),
+    (dict(k=scan.MAX_K + 1, out_stride=scan.MAX_K + 1), INVALID),
+    (dict(out_stride=9), INVALID),
+    (dict(dimension=-1), INVALID),
+    (dict(row_stride=7), INVALID),
+    (dict(query_stride=7), INVALID),
+    (dict(num_rows=-1), INVALID),
+    (dict(ids=FAKE, num_ids=-1), INVALID),
+    (dict(distances=None), INVALID),
+    (dict(nodes=None), INVALID),
+    (dict(rows=None), INVALID),
+    (dict(queries=None), INVALID),
+    (dict(num_rows=1 << 32, row_stride=8), TOO_LARGE),   # node ids are 32-bit, below NO_NODE
+    (dict(num_queries=1 << 31), TOO_LARGE),
+    (dict(num_queries=0), OK),
+])
+def test_top_k_arguments(over, status):
+    lib = _native.scan_library()
+    assert lib.vectra_scan_top_k(ctypes.byref(_top_k_args(**over)), None) == status
+    assert lib.vectra_scan_top_k(None, None) == INVALID
 
 
 def test_wrappers_refuse_cpu_tensors():

@@ -220,3 +220,94 @@ def test_empty_inputs():
                                  torch.zeros(0, 1, dtype=torch.uint8, device='cuda')).shape == (1, 0)
     zero_dim = scan.l2_squared_distances(torch.zeros(1, 0, device='cuda'), torch.zeros(5, 0, device='cuda'))
     assert zero_dim.tolist() == [[0.0] * 5]
+
+
+# Exhaustive k-nearest search (vectra_scan_top_k).
+
+def _check_nearest(query, rows, k, ids=None, msg=''):
+    """The kernel's (distances, nodes) against the oracle: nodes exactly,
+    distances bit for bit (NaN as NaN)."""
+    got_d, got_n = scan.nearest(_gpu(query), _gpu(rows), k, None if ids is None else _gpu(ids))
+    want_d, want_n = oracle.nearest(query, rows, k, ids)
+    np.testing.assert_array_equal(got_n.cpu().numpy(), want_n, err_msg=msg)
+    _same(got_d, want_d, msg)
+
+
+def test_nearest_equals_the_reference_outputs(golden):
+    for case in sorted(int(k.split('_')[2]) for k in golden if k.startswith('near_k_')):
+        ids = golden[f'near_ids_{case}']
+        query, rows, k = golden[f'near_query_{case}'][None], golden[f'near_rows_{case}'], int(golden[f'near_k_{case}'])
+        print(f'nearest fixture case {case}', flush=True)
+        got_d, got_n = scan.nearest(_gpu(query), _gpu(rows), k, _gpu(ids) if ids.size else None)
+        want_d, want_n = golden[f'near_dist_{case}'], golden[f'near_node_{case}']
+        m = want_n.shape[0]
+        np.testing.assert_array_equal(got_n.cpu().numpy()[0, :m], want_n, err_msg=f'case {case}')
+        _same(got_d[0, :m], want_d, f'case {case}')
+        assert (got_n.cpu().numpy()[0, m:] == scan.NO_NODE).all() and torch.isinf(got_d[0, m:]).all()
+
+
+# Up to 1023 queries take 16-wave workgroups, from 1024 on 4-wave ones.
+@pytest.mark.parametrize('n,dim,k,queries', [(2048, 128, 10, 4), (2048, 128, 100, 2), (700, 17, 1, 3),
+                                             (5000, 32, 1024, 2), (300, 300, 64, 2), (100, 0, 20, 2),
+                                             (1, 8, 5, 1), (30, 16, 1024, 1), (300, 24, 16, 1100),
+                                             (2048, 128, 10, 1024)])
+def test_nearest_against_the_oracle(n, dim, k, queries):
+    rng = np.random.default_rng(n + dim + k)
+    rows = rng.standard_normal((n, dim)).astype(np.float32)
+    rows[n // 2: n // 2 + n // 10] = rows[: n // 10]  # equal distances, ranked by node
+    q = rng.standard_normal((queries, dim)).astype(np.float32)
+    print(f'nearest n={n} dim={dim} k={k} queries={queries}', flush=True)
+    _check_nearest(q, rows, k, msg=f'n={n} dim={dim} k={k}')
+
+
+def test_nearest_with_candidate_ids_and_special_values():
+    rng = np.random.default_rng(3)
+    n, dim = 900, 40
+    rows = rng.standard_normal((n, dim)).astype(np.float32)
+    rows[5, 3] = np.nan     # a NaN distance: after every number
+    rows[6, 0] = np.inf     # an infinite distance
+    rows[7] = 0.0
+    q = rng.standard_normal((3, dim)).astype(np.float32)
+    ids = rng.integers(0, n + 200, 1500).astype(np.uint32)  # some past the row count: skipped
+    ids[:100] = ids[100:200]                                # duplicates: kept
+    ids[200:203] = [5, 6, 7]
+    for k in (1, 16, 257, 1024):
+        print(f'nearest ids k={k}', flush=True)
+        _check_nearest(q, rows, k, ids, msg=f'ids k={k}')
+    # A query equal to a row: distance exactly 0 first.
+    q2 = rows[[11]].copy()
+    d, nodes = scan.nearest(_gpu(q2), _gpu(rows), 3)
+    assert d[0, 0].item() == 0.0 and nodes[0, 0].item() == 11
+
+
+def test_nearest_keeps_up_when_every_candidate_is_better():
+    """Distances falling with the row index: every candidate beats the k-th
+    best so far, so the kernel merges its buffer again and again."""
+    dim, n, k = 16, 6000, 1024
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((1, dim)).astype(np.float32)
+    u = np.zeros(dim, np.float32)
+    u[0] = 1.0
+    rows = (q + np.outer((n - np.arange(n)) * 0.01, u)).astype(np.float32)
+    _check_nearest(q, rows, k, msg='descending')
+
+
+def test_nearest_over_a_large_shard():
+    rng = np.random.default_rng(21)
+    rows = rng.standard_normal((200_000, 128)).astype(np.float32)
+    q = rng.standard_normal((2, 128)).astype(np.float32)
+    print('nearest over 200k rows', flush=True)
+    _check_nearest(q, rows, 10, msg='200k rows')
+
+
+def test_nearest_matches_the_row_scan_and_a_sort():
+    """The distances are the row scan's, bit for bit, and the nodes a stable
+    sort of them."""
+    rng = np.random.default_rng(4)
+    rows = _gpu(rng.standard_normal((3000, 96)).astype(np.float32))
+    q = _gpu(rng.standard_normal((5, 96)).astype(np.float32))
+    d, nodes = scan.nearest(q, rows, 50)
+    full = scan.l2_squared_distances(q, rows)
+    order = torch.from_numpy(np.argsort(full.cpu().numpy(), axis=1, kind='stable')[:, :50])
+    assert torch.equal(nodes.cpu().to(torch.int64), order)
+    _same(d, torch.gather(full.cpu(), 1, order))

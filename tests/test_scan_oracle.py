@@ -212,3 +212,82 @@ def test_planted_mistakes_fail_the_bit_level_pin(golden):
     assert adc_bad > 0
     # The correct restatement matches on the same cases.
     assert mismatches(scan.l2_squared, 'rows_', 'l2') == 0
+
+
+# ExhaustiveSearch's selection: the k nearest under CloserFirst.
+
+def _nearest_case(golden, case):
+    ids = golden[f'near_ids_{case}']
+    return (golden[f'near_query_{case}'][None], golden[f'near_rows_{case}'], int(golden[f'near_k_{case}']),
+            ids if ids.size else None, golden[f'near_dist_{case}'], golden[f'near_node_{case}'])
+
+
+def test_nearest_matches_the_reference_fixture(golden):
+    cases = sorted(int(k.split('_')[2]) for k in golden if k.startswith('near_k_'))
+    assert len(cases) >= 5
+    for case in cases:
+        query, rows, k, ids, want_d, want_n = _nearest_case(golden, case)
+        got_d, got_n = scan.nearest(query, rows, k, ids)
+        m = want_n.shape[0]
+        np.testing.assert_array_equal(_bits(got_d[0, :m]), _bits(want_d), err_msg=f'case {case}')
+        np.testing.assert_array_equal(got_n[0, :m], want_n, err_msg=f'case {case}')
+        # Past the candidates: empty slots.
+        assert np.isposinf(got_d[0, m:]).all() and (got_n[0, m:] == scan.NO_NODE).all()
+
+
+def test_nearest_matches_the_reference_build(ref):
+    ref.ref_nearest.restype = ctypes.c_int64
+    rng = np.random.default_rng(77)
+    for n, dim, k in ((500, 24, 1), (500, 24, 37), (64, 3, 64), (1000, 130, 200)):
+        rows = rng.standard_normal((n, dim)).astype(np.float32)
+        rows[n // 3: n // 3 + 20] = rows[:20]  # ties
+        query = rng.standard_normal(dim).astype(np.float32)
+        dist = _ref_rows(ref, 0, query, rows)
+        nodes = np.arange(n, dtype=np.uint32)
+        want_d, want_n = np.zeros(k, np.float32), np.zeros(k, np.uint32)
+        m = ref.ref_nearest(_p(dist), _p(nodes), ctypes.c_int64(n), ctypes.c_int64(k), _p(want_d), _p(want_n))
+        got_d, got_n = scan.nearest(query[None], rows, k)
+        np.testing.assert_array_equal(_bits(got_d[0, :m]), _bits(want_d[:m]))
+        np.testing.assert_array_equal(got_n[0, :m], want_n[:m])
+
+
+def test_nearest_by_brute_force():
+    """Tiny cases against Python's sort of (distance, node) pairs, with the
+    candidate rules written out: ids past the row count skipped, duplicates
+    kept, NaN after every number."""
+    rng = np.random.default_rng(5)
+    for trial in range(40):
+        n, dim = int(rng.integers(1, 12)), int(rng.integers(0, 6))
+        rows = rng.integers(-2, 3, (n, dim)).astype(np.float32)  # small integers: many equal distances
+        if trial % 5 == 0 and dim:
+            rows[rng.integers(n), 0] = np.nan
+        query = rng.integers(-2, 3, dim).astype(np.float32)
+        ids = rng.integers(0, n + 3, int(rng.integers(0, 15))).astype(np.uint32) if trial % 2 else None
+        k = int(rng.integers(1, 16))
+        cand = list(range(n)) if ids is None else [int(i) for i in ids if i < n]
+        pairs = []
+        for node in cand:
+            d = float(np.float32(sum(float(np.float32(q - r)) ** 2 for q, r in zip(query, rows[node]))))
+            pairs.append((np.isnan(d), 0.0 if np.isnan(d) else d, node))
+        pairs.sort()
+        got_d, got_n = scan.nearest(query[None], rows, k, ids)
+        for r in range(k):
+            if r < len(pairs):
+                nan, d, node = pairs[r]
+                assert got_n[0, r] == node, (trial, r)
+                assert np.isnan(got_d[0, r]) if nan else got_d[0, r] == d, (trial, r)
+            else:
+                assert got_n[0, r] == scan.NO_NODE and np.isposinf(got_d[0, r])
+
+
+def test_a_planted_tie_mistake_fails_the_fixture(golden, monkeypatch):
+    """Ties broken by descending node id (or left in scan order) fail the pin."""
+    query, rows, k, ids, want_d, want_n = _nearest_case(golden, 4)
+    real_lexsort = np.lexsort
+
+    def descending_ties(keys):
+        nodes, d, nan = keys
+        return real_lexsort((-nodes, d, nan))
+    monkeypatch.setattr(scan.np, 'lexsort', descending_ties)
+    _, got_n = scan.nearest(query, rows, k, ids)
+    assert not np.array_equal(got_n[0, :want_n.shape[0]], want_n)

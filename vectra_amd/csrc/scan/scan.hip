@@ -386,6 +386,180 @@ int launch_rows(RowScan& p, hipStream_t stream) {
   return p.ids != nullptr ? launch_rows_ids<kMetric, true>(p, stream) : launch_rows_ids<kMetric, false>(p, stream);
 }
 
+
+// ---------------------------------------------------------------- top k
+
+// Exhaustive k-nearest search (ShardIndex::ExhaustiveSearch,
+// shard_index.cc:236-264): one workgroup per query scans every candidate
+// with the row scan's L2 arithmetic (the same operations in the same order,
+// so the distances are bit-identical) and keeps the k nearest.  The order is
+// CloserFirst's (search_scratch.h: distance ascending, ties by node id),
+// which a 64-bit key turns into integer order: the distance's bits mapped so
+// that unsigned order follows float order, above the node id.  The workgroup
+// holds the k best keys and the candidates that beat the k-th since the last
+// merge in LDS; when those could overflow the buffer, and at the end, the
+// keys are sorted (bitonic) and the first k kept.  No device memory besides
+// the inputs and outputs.
+struct TopK {
+  const float* queries;
+  const float* rows;
+  const uint32_t* ids;
+  float* distances;
+  uint32_t* nodes;
+  int64_t query_stride, row_stride, out_stride;
+  int64_t num_rows, num_cand;
+  int32_t dim, k;
+};
+
+constexpr int kTopKKeys = 2048;        // LDS keys: the k best, then the new candidates
+constexpr int kTopKCands = 4;          // candidates a 16-lane group loads together
+constexpr int kTopKRound = 256;        // candidates between merge checks
+constexpr uint64_t kNoKey = ~uint64_t{0};  // an empty slot (above every real key)
+static_assert(kTopKKeys - VECTRA_SCAN_MAX_K >= kTopKRound, "room for a round of candidates");
+// Workgroups of 4 waves when there are queries enough to fill the device
+// with them; otherwise 16, so that one query's candidates are loaded 4
+// times as wide and its sorts run on 4 times the threads.
+constexpr int64_t kTopKWideBelow = 1024;  // queries
+
+// Candidates ranked by (distance, node).  -0 ranks as +0 (CloserFirst
+// compares values), and every NaN as one quiet NaN above +inf.
+__device__ __forceinline__ uint64_t nearest_key(float d, uint32_t node) {
+  uint32_t b = __float_as_uint(d);
+  if (d != d) b = 0x7fc00000u;
+  else if (b == 0x80000000u) b = 0u;
+  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return (static_cast<uint64_t>(ord) << 32) | node;
+}
+__device__ __forceinline__ float key_distance(uint64_t key) {
+  const uint32_t ord = static_cast<uint32_t>(key >> 32);
+  return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
+}
+
+template <bool kIds, int kTopKThreads>
+__global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
+  constexpr int kTopKGroups = kTopKThreads / kLanes;
+  constexpr int kSteps = kTopKRound / (kTopKGroups * kTopKCands);  // loads a group issues per round
+  static_assert(kSteps * kTopKGroups * kTopKCands == kTopKRound, "whole steps per round");
+  __shared__ uint64_t keys[kTopKKeys];
+  __shared__ uint32_t fill;  // candidates in keys[k ..] since the last merge
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & (kLanes - 1);
+  const int group = tid / kLanes;
+  const int64_t q = blockIdx.x;
+  const int k = p.k;
+  const int full = p.dim - p.dim % kLanes;
+  const int tail = p.dim - full;
+  const float* qlane = p.queries + q * p.query_stride + lane;
+
+  for (int i = tid; i < kTopKKeys; i += kTopKThreads) keys[i] = kNoKey;
+  if (tid == 0) fill = 0;
+  __syncthreads();
+
+  // Sorts keys[0 .. k + n) ascending (padded with empty slots to a power of
+  // two), leaving the k best in keys[0 .. k); every thread takes part.
+  auto merge = [&](int n) {
+    int size = 2;
+    while (size < k + n) size <<= 1;
+    for (int i = k + n + tid; i < size; i += kTopKThreads) keys[i] = kNoKey;
+    __syncthreads();
+    for (int span = 2; span <= size; span <<= 1) {
+      for (int stride = span >> 1; stride > 0; stride >>= 1) {
+        for (int t = tid; t < size / 2; t += kTopKThreads) {
+          const int i = 2 * t - (t & (stride - 1));
+          const int j = i + stride;
+          const uint64_t a = keys[i], b = keys[j];
+          if ((a > b) == ((i & span) == 0)) {
+            keys[i] = b;
+            keys[j] = a;
+          }
+        }
+        __syncthreads();
+      }
+    }
+  };
+
+  uint64_t worst = kNoKey;  // the k-th best key so far; empty while fewer than k
+  for (int64_t base = 0; base < p.num_cand; base += kTopKRound) {
+    // A round: kSteps steps of kTopKCands candidates per 16-lane group, a
+    // step's loads issued before any of its sums (each candidate's own
+    // operations keep the row scan's order).
+    for (int s = 0; s < kSteps; ++s) {
+      bool valid[kTopKCands];
+      const float* rlane[kTopKCands];
+      int64_t row[kTopKCands];
+#pragma unroll
+      for (int c = 0; c < kTopKCands; ++c) {
+        const int64_t cand = base + static_cast<int64_t>(s * kTopKCands + c) * kTopKGroups + group;
+        valid[c] = cand < p.num_cand;
+        row[c] = valid[c] ? cand : 0;
+        if constexpr (kIds) {
+          const uint32_t id = valid[c] ? p.ids[cand] : 0u;
+          valid[c] = valid[c] && static_cast<int64_t>(id) < p.num_rows;
+          row[c] = valid[c] ? id : 0;
+        }
+        rlane[c] = p.rows + row[c] * p.row_stride + lane;
+      }
+      float acc[kTopKCands];
+#pragma unroll
+      for (int c = 0; c < kTopKCands; ++c) acc[c] = 0.f;
+      int i = 0;
+      for (; i + kLanes * kUnroll <= full; i += kLanes * kUnroll) {
+        float rv[kTopKCands][kUnroll], qv[kUnroll];
+#pragma unroll
+        for (int c = 0; c < kTopKCands; ++c)
+#pragma unroll
+          for (int u = 0; u < kUnroll; ++u) rv[c][u] = valid[c] ? rlane[c][i + kLanes * u] : 0.f;
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) qv[u] = qlane[i + kLanes * u];
+#pragma unroll
+        for (int c = 0; c < kTopKCands; ++c)
+#pragma unroll
+          for (int u = 0; u < kUnroll; ++u) acc[c] = acc[c] + term<VECTRA_SCAN_L2_SQUARED>(qv[u], rv[c][u]);
+      }
+      for (; i < full; i += kLanes) {
+        const float qi = qlane[i];
+#pragma unroll
+        for (int c = 0; c < kTopKCands; ++c)
+          acc[c] = acc[c] + term<VECTRA_SCAN_L2_SQUARED>(qi, valid[c] ? rlane[c][i] : 0.f);
+      }
+#pragma unroll
+      for (int c = 0; c < kTopKCands; ++c) {
+        float sum = acc[c];
+#pragma unroll
+        for (int width = kLanes / 2; width > 0; width /= 2) {
+          const float other = __shfl_down(sum, width, kLanes);
+          if (lane < width) sum = sum + other;
+        }
+        float t = 0.f;
+        if (valid[c] && lane < tail) t = term<VECTRA_SCAN_L2_SQUARED>(qlane[full], rlane[c][full]);
+        for (int e = 0; e < tail; ++e) sum = sum + __shfl(t, e, kLanes);
+        if (valid[c] && lane == 0) {
+          const uint64_t key = nearest_key(sum, static_cast<uint32_t>(row[c]));
+          if (key < worst) keys[k + atomicAdd(&fill, 1u)] = key;
+        }
+      }
+    }
+    __syncthreads();
+    const int n = static_cast<int>(fill);
+    // Merge once k candidates are in hand (the threshold then discards most
+    // of the rest), and whenever the next round might not fit.
+    if ((worst == kNoKey && n >= k) || n > kTopKKeys - k - kTopKRound) {
+      merge(n);
+      if (tid == 0) fill = 0;
+      worst = keys[k - 1];
+      __syncthreads();
+    }
+  }
+  const int n = static_cast<int>(fill);
+  if (n > 0) merge(n);
+  for (int r = tid; r < k; r += kTopKThreads) {
+    const uint64_t key = keys[r];
+    const int64_t off = q * p.out_stride + r;
+    p.distances[off] = key == kNoKey ? INFINITY : key_distance(key);
+    p.nodes[off] = key == kNoKey ? VECTRA_SCAN_NO_NODE : static_cast<uint32_t>(key);
+  }
+}
+
 }  // namespace
 }  // namespace vectra_scan
 
@@ -501,6 +675,48 @@ extern "C" int vectra_scan_pq_adc(const vectra_pq_adc_args* a, hipStream_t strea
   }
   return launched(
       hipLaunchKernel(reinterpret_cast<const void*>(&pq_adc_kernel<false>), grid, dim3(kThreads), args, 0, stream));
+}
+
+extern "C" int vectra_scan_top_k(const vectra_scan_top_k_args* a, hipStream_t stream) {
+  if (a == nullptr) return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (a->dimension < 0 || a->num_queries < 0 || a->num_rows < 0 || (a->ids != nullptr && a->num_ids < 0))
+    return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (a->k < 1 || a->k > VECTRA_SCAN_MAX_K) return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (a->row_stride < a->dimension || a->query_stride < a->dimension || a->out_stride < a->k)
+    return VECTRA_SCAN_INVALID_ARGUMENT;
+  if (a->num_queries == 0) return VECTRA_SCAN_OK;
+  const int64_t cand = a->ids != nullptr ? a->num_ids : a->num_rows;
+  const bool reads = a->dimension > 0 && cand > 0;
+  if (a->distances == nullptr || a->nodes == nullptr || (reads && (a->queries == nullptr || a->rows == nullptr)))
+    return VECTRA_SCAN_INVALID_ARGUMENT;
+  // Node ids are 32-bit, below VECTRA_SCAN_NO_NODE; one workgroup per query.
+  if (a->num_rows > int64_t{VECTRA_SCAN_NO_NODE} || a->num_queries > 0x7fffffffLL) return VECTRA_SCAN_TOO_LARGE;
+  const int64_t lim = int64_t{1} << 62;
+  if ((a->num_rows > 0 && a->row_stride > lim / a->num_rows) || a->out_stride > lim / a->num_queries ||
+      a->query_stride > lim / a->num_queries)
+    return VECTRA_SCAN_TOO_LARGE;
+  TopK p;
+  p.queries = a->queries;
+  p.rows = a->rows;
+  p.ids = a->ids;
+  p.distances = a->distances;
+  p.nodes = a->nodes;
+  p.query_stride = a->query_stride;
+  p.row_stride = a->row_stride;
+  p.out_stride = a->out_stride;
+  p.num_rows = a->num_rows;
+  p.num_cand = cand;
+  p.dim = a->dimension;
+  p.k = a->k;
+  void* args[] = {&p};
+  const bool wide = a->num_queries < kTopKWideBelow;
+  const void* kernel = a->ids != nullptr
+                           ? (wide ? reinterpret_cast<const void*>(&scan_top_k_kernel<true, 1024>)
+                                   : reinterpret_cast<const void*>(&scan_top_k_kernel<true, 256>))
+                           : (wide ? reinterpret_cast<const void*>(&scan_top_k_kernel<false, 1024>)
+                                   : reinterpret_cast<const void*>(&scan_top_k_kernel<false, 256>));
+  return launched(hipLaunchKernel(kernel, dim3(static_cast<unsigned>(a->num_queries)), dim3(wide ? 1024 : 256), args,
+                                  0, stream));
 }
 
 extern "C" const char* vectra_scan_status_string(int status) {

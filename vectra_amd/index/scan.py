@@ -18,6 +18,9 @@ pq_distance_tables       ProductQuantizer::ComputeDistanceTable
                          (pq_codec.cc:208-217)
 pq_adc_distances         PqAdcDistance (simd_distance.cc:68-81), per code
                          (hnsw_searcher.h:74; tests/tools/index_study.cc:82)
+nearest                  ShardIndex::ExhaustiveSearch's results
+                         (shard_index.cc:236-264): the k nearest by
+                         L2SquaredDistance in CloserFirst order
 =======================  ==================================================
 
 Arguments are torch tensors on the GPU: float32 vectors as [count, dimension]
@@ -36,6 +39,8 @@ from vectra_amd.kernels import _native
 
 L2_SQUARED, INNER_PRODUCT, SQUARED_NORM = 0, 1, 2
 PQ_CENTROIDS = 256
+MAX_K = 1024            # VECTRA_SCAN_MAX_K
+NO_NODE = 0xFFFFFFFF    # VECTRA_SCAN_NO_NODE: an empty result slot
 _OK, _INVALID = 0, 1
 
 
@@ -69,6 +74,16 @@ class _PqAdcArgs(ctypes.Structure):
         ('codes', ctypes.c_void_p), ('num_codes', ctypes.c_int64), ('code_stride', ctypes.c_int64),
         ('ids', ctypes.c_void_p), ('num_ids', ctypes.c_int64),
         ('out', ctypes.c_void_p), ('out_stride', ctypes.c_int64),
+    ]
+
+
+class _TopKArgs(ctypes.Structure):
+    _fields_ = [
+        ('dimension', ctypes.c_int32), ('k', ctypes.c_int32),
+        ('queries', ctypes.c_void_p), ('num_queries', ctypes.c_int64), ('query_stride', ctypes.c_int64),
+        ('rows', ctypes.c_void_p), ('num_rows', ctypes.c_int64), ('row_stride', ctypes.c_int64),
+        ('ids', ctypes.c_void_p), ('num_ids', ctypes.c_int64),
+        ('distances', ctypes.c_void_p), ('nodes', ctypes.c_void_p), ('out_stride', ctypes.c_int64),
     ]
 
 
@@ -203,3 +218,29 @@ def pq_adc_distances(tables: torch.Tensor, codes: torch.Tensor, ids=None, out=No
     with torch.cuda.device(codes.device):
         _check(_native.scan_library().vectra_scan_pq_adc(ctypes.byref(args), _stream(codes.device)))
     return out
+
+
+def nearest(queries: torch.Tensor, rows: torch.Tensor, k: int, ids=None):
+    """ExhaustiveSearch for each query: (distances [num_queries, k] float32,
+    nodes [num_queries, k] uint32), nearest first by (distance, node id).
+
+    Candidates are rows ids[i] (ids not below the row count are skipped,
+    duplicates kept) or every row; slots past the number of candidates hold
+    +inf and NO_NODE.  k is 1 .. MAX_K."""
+    queries = _matrix(queries, 'queries', torch.float32)
+    rows = _matrix(rows, 'rows', torch.float32)
+    if queries.shape[1] != rows.shape[1]:
+        raise ValueError('queries and rows must have the same dimension')
+    if not 1 <= k <= MAX_K:
+        raise ValueError(f'k must be in [1, {MAX_K}]')
+    ids = _ids(ids, rows)
+    n_q = queries.shape[0]
+    distances = torch.empty((n_q, k), dtype=torch.float32, device=rows.device)
+    nodes = torch.empty((n_q, k), dtype=torch.uint32, device=rows.device)
+    args = _TopKArgs(rows.shape[1], k, queries.data_ptr(), n_q, _row_stride(queries),
+                     rows.data_ptr(), rows.shape[0], _row_stride(rows),
+                     None if ids is None else ids.data_ptr(), 0 if ids is None else ids.shape[0],
+                     distances.data_ptr(), nodes.data_ptr(), k)
+    with torch.cuda.device(rows.device):
+        _check(_native.scan_library().vectra_scan_top_k(ctypes.byref(args), _stream(rows.device)))
+    return distances, nodes

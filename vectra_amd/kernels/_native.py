@@ -77,7 +77,7 @@ def hip_library() -> ctypes.CDLL:
 def scan_library() -> ctypes.CDLL:
     """The distance-scan library as a ctypes handle."""
     lib = ctypes.CDLL(_require(SCAN_LIBRARY))
-    for name in ('vectra_scan_rows', 'vectra_pq_distance_tables', 'vectra_scan_pq_adc'):
+    for name in ('vectra_scan_rows', 'vectra_pq_distance_tables', 'vectra_scan_pq_adc', 'vectra_scan_top_k'):
         fn = getattr(lib, name)
         fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         fn.restype = ctypes.c_int
