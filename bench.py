@@ -275,6 +275,7 @@ def load_profile(name):
 
 REF_SCAN = os.path.join(ROOT, 'oracle', '_ref', 'libref_scan.so')
 SCAN_CPU_ROWS = 65536  # rows (codes, tables) per CPU call and in the numerics sample
+SCAN_CPU_TOPK_QUERIES = 16  # queries per CPU call of a top-k workload, and in its numerics sample
 
 
 def _scan_cpu(w, inputs):
@@ -302,6 +303,30 @@ def _scan_cpu(w, inputs):
                 else:
                     out[q] = oracle.l2_squared(queries[q], rows)
             return out
+        return run, queries.shape[0] * n, ('reference' if lib is not None else 'port')
+    if w.kind == 'topk':
+        # ExhaustiveSearch per query: the distance to every row, then the k
+        # nearest under the reference's CloserFirst (oracle/_ref's shim over
+        # its header), or the numpy restatement.
+        rows = np.ascontiguousarray(inputs['rows'].cpu().numpy())
+        queries = np.ascontiguousarray(inputs['queries'][:SCAN_CPU_TOPK_QUERIES].cpu().numpy())
+        n = rows.shape[0]
+        nodes = np.arange(n, dtype=np.uint32)
+        if lib is not None:
+            lib.ref_nearest.restype = ctypes.c_int64
+
+        def run():
+            if lib is None:
+                return oracle.nearest(queries, rows, w.k)
+            out_d = np.full((queries.shape[0], w.k), np.inf, np.float32)
+            out_n = np.full((queries.shape[0], w.k), oracle.NO_NODE, np.uint32)
+            dist = np.empty(n, np.float32)
+            for q in range(queries.shape[0]):
+                lib.ref_scan_rows(0, ptr(queries[q]), ptr(rows), ctypes.c_int64(n), ctypes.c_int64(w.dim), w.dim,
+                                  ptr(dist))
+                lib.ref_nearest(ptr(dist), ptr(nodes), ctypes.c_int64(n), ctypes.c_int64(w.k), ptr(out_d[q]),
+                                ptr(out_n[q]))
+            return out_d, out_n
         return run, queries.shape[0] * n, ('reference' if lib is not None else 'port')
     if w.kind == 'adc':
         codes = np.ascontiguousarray(inputs['codes'][:SCAN_CPU_ROWS].cpu().numpy())
@@ -354,10 +379,18 @@ def scan_main(args):
         got = scan_workloads.launch(w, sets[0], out)
         torch.cuda.synchronize()
         want = cpu_run()
-        got = got[:want.shape[0], :want.shape[1]].cpu().numpy()
-        if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+        if w.kind == 'topk':  # (distances, nodes) of the sampled queries
+            got = tuple(t[:want[0].shape[0]].cpu().numpy() for t in got)
+            same = (np.array_equal(got[0].view(np.uint32), want[0].view(np.uint32))
+                    and np.array_equal(got[1], want[1]))
+            size = want[0].size
+        else:
+            got = got[:want.shape[0], :want.shape[1]].cpu().numpy()
+            same = np.array_equal(got.view(np.uint32), want.view(np.uint32))
+            size = want.size
+        if not same:
             raise SystemExit('numerics gate: the scan differs from the CPU reference')
-        log(f'numerics gate passed: {want.size} outputs bit-identical to the {cpu_kind} CPU code')
+        log(f'numerics gate passed: {size} outputs bit-identical to the {cpu_kind} CPU code')
 
     stream = torch.cuda.current_stream()
 
@@ -387,15 +420,24 @@ def scan_main(args):
 
     nbytes = w.algorithmic_bytes()
     achieved = nbytes / seconds / 1e9
-    line_roof = {'bound': 'hbm', 'achieved': achieved, 'peak': roofline.MI355X.hbm_bytes_per_s / 1e9,
-                 'unit': 'GB/s', 'kernel': scan_workloads.KERNEL_NAMES[w.kind], 'traffic': None,
-                 'algorithmic_bytes': nbytes}
-    line_roof['frac'] = achieved / line_roof['peak']
+    if w.kind == 'topk':
+        # Rows re-read by every query from the L2 caches: bound by the vector
+        # ALU (three fp32 operations per dimension of each distance).
+        terms = w.queries * w.count * w.dim
+        line_roof = {'bound': 'valu', 'achieved': 3 * terms / seconds / 1e12,
+                     'peak': scan_workloads.VALU_LANE_OPS_PER_S / 1e12, 'unit': 'T lane-ops/s',
+                     'kernel': scan_workloads.KERNEL_NAMES[w.kind], 'traffic': None, 'algorithmic_bytes': nbytes,
+                     'hbm_GB/s': achieved}
+    else:
+        line_roof = {'bound': 'hbm', 'achieved': achieved, 'peak': roofline.MI355X.hbm_bytes_per_s / 1e9,
+                     'unit': 'GB/s', 'kernel': scan_workloads.KERNEL_NAMES[w.kind], 'traffic': None,
+                     'algorithmic_bytes': nbytes}
+    line_roof['frac'] = line_roof['achieved'] / line_roof['peak']
     measured = load_profile(f'traffic_scan_{w.name}.json')
     if measured is not None and measured.get('kernel') == line_roof['kernel']:
         line_roof['traffic'] = measured['traffic_bytes']
         line_roof['traffic_source'] = f'profiles/traffic_scan_{w.name}.json'
-    if not args.no_read_ceiling and nbytes >= (1 << 20):
+    if not args.no_read_ceiling and nbytes >= (1 << 20) and w.kind != 'topk':
         from vectra_amd.benchmarks import read_ceiling  # noqa: E402
 
         ceiling = read_ceiling.measure(nbytes)
@@ -410,7 +452,7 @@ def scan_main(args):
         'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': ms,
         'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32', 'data': 'synthetic',
         'config': {'workload': f'{w.name}: {w.kind}, queries={w.queries} count={w.count} dim={w.dim} '
-                               f'subspaces={w.subspaces}',
+                               f'subspaces={w.subspaces}' + (f' k={w.k}' if w.k else ''),
                    'input_sets': n_sets, 'trials': len(trial_ms), 'lead_in_launches': lead_steps},
         'roofline': line_roof,
         'cpu_baseline': cpu,

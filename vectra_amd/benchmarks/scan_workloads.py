@@ -15,7 +15,17 @@ pq_shard      PqAdcDistance of one query table over 4,000,000 16-byte codes
               (the ADC pass of a search over a whole shard)
 pq_tables     ComputeDistanceTable for 1,024 queries (dimension 128,
               16 sub-spaces)
+exhaustive_   ShardIndex::ExhaustiveSearch for 1,024 queries at once, each
+topk          over the same 2,048 rows (exhaustive_scan_threshold), k = 10:
+              the k nearest in CloserFirst order
+single_topk   the same for one query (the engine's per-request case)
 ============  ===============================================================
+
+The top-k workloads read the same rows for every query (the L2 caches
+serve them after the first), so their bound is the vector ALU rather than
+HBM: three fp32 operations (subtract, multiply, add) per dimension of each
+distance, against the 39.3 T lane operations per second of MI355X's vector
+units (256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz, unpacked fp32).
 
 Algorithmic bytes per launch count every input byte once and every output
 byte once: rows (or codes, or codebooks), queries (or tables) and the
@@ -42,6 +52,7 @@ class Workload:
     dim: int = 128
     subspaces: int = 16
     unit: str = 'distances/s'
+    k: int = 0           # nearest rows kept per query ('topk')
 
     def algorithmic_bytes(self) -> int:
         if self.kind == 'rows':
@@ -49,6 +60,8 @@ class Workload:
         if self.kind == 'adc':
             return (self.count * self.subspaces + self.queries * self.subspaces * PQ_CENTROIDS * 4
                     + self.queries * self.count * 4)
+        if self.kind == 'topk':  # rows and queries in, k (distance, node) pairs out
+            return self.count * self.dim * 4 + self.queries * self.dim * 4 + self.queries * self.k * 8
         # tables: queries + codebooks in, tables out
         return (self.queries * self.dim * 4 + PQ_CENTROIDS * self.dim * 4
                 + self.queries * self.subspaces * PQ_CENTROIDS * 4)
@@ -59,7 +72,7 @@ class Workload:
         return self.queries * self.count
 
     def set_bytes(self) -> int:
-        if self.kind == 'rows':
+        if self.kind in ('rows', 'topk'):
             return self.count * self.dim * 4
         if self.kind == 'adc':
             return self.count * self.subspaces
@@ -72,10 +85,14 @@ WORKLOADS = {w.name: w for w in (
     Workload('exhaustive', 'rows', 1, 2048),
     Workload('pq_shard', 'adc', 1, 4_000_000),
     Workload('pq_tables', 'tables', 1024, 0, unit='table entries/s'),
+    Workload('exhaustive_topk', 'topk', 1024, 2048, k=10),
+    Workload('single_topk', 'topk', 1, 2048, k=10),
 )}
 
 # The kernel each workload runs (pq_shard's 16-byte codes take the 16-byte-load ADC kernel).
-KERNEL_NAMES = {'rows': 'scan_rows_kernel', 'adc': 'pq_adc_vec_kernel', 'tables': 'pq_table_kernel'}
+KERNEL_NAMES = {'rows': 'scan_rows_kernel', 'adc': 'pq_adc_vec_kernel', 'tables': 'pq_table_kernel',
+                'topk': 'scan_top_k_kernel'}
+VALU_LANE_OPS_PER_S = 256 * 4 * 16 * 2.4e9  # MI355X vector units, unpacked fp32
 
 
 def sets_needed(w: Workload) -> int:
@@ -87,7 +104,7 @@ def make_sets(w: Workload, seed: int = 0, device='cuda') -> list[dict]:
     gen = torch.Generator(device='cpu').manual_seed(seed)
     n_sets = sets_needed(w)
     sets = []
-    if w.kind == 'rows':
+    if w.kind in ('rows', 'topk'):
         # One host draw, varied per set on the device (scaled), to keep set-up fast.
         base = torch.randn(w.count, w.dim, generator=gen).to(device)
         for i in range(n_sets):
@@ -106,7 +123,10 @@ def make_sets(w: Workload, seed: int = 0, device='cuda') -> list[dict]:
     return sets
 
 
-def make_output(w: Workload, device='cuda') -> torch.Tensor:
+def make_output(w: Workload, device='cuda'):
+    if w.kind == 'topk':
+        return (torch.empty(w.queries, w.k, device=device), torch.empty(w.queries, w.k, dtype=torch.uint32,
+                                                                        device=device))
     if w.kind == 'tables':
         return torch.empty(w.queries, w.subspaces * PQ_CENTROIDS, device=device)
     return torch.empty(w.queries, w.count, device=device)
@@ -116,6 +136,8 @@ def launch(w: Workload, inputs: dict, out: torch.Tensor) -> torch.Tensor:
     """One launch of the workload's kernel on the current stream."""
     if w.kind == 'rows':
         return scan.l2_squared_distances(inputs['queries'], inputs['rows'], out=out)
+    if w.kind == 'topk':
+        return scan.nearest(inputs['queries'], inputs['rows'], w.k, out=out)
     if w.kind == 'adc':
         return scan.pq_adc_distances(inputs['tables'], inputs['codes'], out=out)
     return scan.pq_distance_tables(inputs['queries'], inputs['codebooks'], w.subspaces, out=out)

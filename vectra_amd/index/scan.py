@@ -220,13 +220,14 @@ def pq_adc_distances(tables: torch.Tensor, codes: torch.Tensor, ids=None, out=No
     return out
 
 
-def nearest(queries: torch.Tensor, rows: torch.Tensor, k: int, ids=None):
+def nearest(queries: torch.Tensor, rows: torch.Tensor, k: int, ids=None, out=None):
     """ExhaustiveSearch for each query: (distances [num_queries, k] float32,
     nodes [num_queries, k] uint32), nearest first by (distance, node id).
 
     Candidates are rows ids[i] (ids not below the row count are skipped,
     duplicates kept) or every row; slots past the number of candidates hold
-    +inf and NO_NODE.  k is 1 .. MAX_K."""
+    +inf and NO_NODE.  k is 1 .. MAX_K.  `out` may give the two output
+    tensors (contiguous, of those shapes and dtypes)."""
     queries = _matrix(queries, 'queries', torch.float32)
     rows = _matrix(rows, 'rows', torch.float32)
     if queries.shape[1] != rows.shape[1]:
@@ -235,8 +236,15 @@ def nearest(queries: torch.Tensor, rows: torch.Tensor, k: int, ids=None):
         raise ValueError(f'k must be in [1, {MAX_K}]')
     ids = _ids(ids, rows)
     n_q = queries.shape[0]
-    distances = torch.empty((n_q, k), dtype=torch.float32, device=rows.device)
-    nodes = torch.empty((n_q, k), dtype=torch.uint32, device=rows.device)
+    if out is None:
+        distances = torch.empty((n_q, k), dtype=torch.float32, device=rows.device)
+        nodes = torch.empty((n_q, k), dtype=torch.uint32, device=rows.device)
+    else:
+        distances, nodes = out
+        for t, dtype in ((distances, torch.float32), (nodes, torch.uint32)):
+            _on_gpu(t, 'out')
+            if t.dtype != dtype or tuple(t.shape) != (n_q, k) or not t.is_contiguous():
+                raise ValueError(f'out must be contiguous ({n_q}, {k}) float32 and uint32 tensors')
     args = _TopKArgs(rows.shape[1], k, queries.data_ptr(), n_q, _row_stride(queries),
                      rows.data_ptr(), rows.shape[0], _row_stride(rows),
                      None if ids is None else ids.data_ptr(), 0 if ids is None else ids.shape[0],
