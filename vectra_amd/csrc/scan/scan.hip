@@ -412,10 +412,7 @@ struct TopK {
 };
 
 constexpr int kTopKKeys = 2048;        // LDS keys: the k best, then the new candidates
-constexpr int kTopKCands = 4;          // candidates a 16-lane group loads together
-constexpr int kTopKRound = 256;        // candidates between merge checks
 constexpr uint64_t kNoKey = ~uint64_t{0};  // an empty slot (above every real key)
-static_assert(kTopKKeys - VECTRA_SCAN_MAX_K >= kTopKRound, "room for a round of candidates");
 // Workgroups of 4 waves when there are queries enough to fill the device
 // with them; otherwise 16, so that one query's candidates are loaded 4
 // times as wide and its sorts run on 4 times the threads.
@@ -435,11 +432,13 @@ __device__ __forceinline__ float key_distance(uint64_t key) {
   return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
 }
 
-template <bool kIds, int kTopKThreads>
+// kTopKThreads threads; a 16-lane group loads kTopKCands candidates at once,
+// kSteps times per round of candidates between merge checks.
+template <bool kIds, int kTopKThreads, int kTopKCands, int kSteps>
 __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
   constexpr int kTopKGroups = kTopKThreads / kLanes;
-  constexpr int kSteps = kTopKRound / (kTopKGroups * kTopKCands);  // loads a group issues per round
-  static_assert(kSteps * kTopKGroups * kTopKCands == kTopKRound, "whole steps per round");
+  constexpr int kTopKRound = kTopKGroups * kTopKCands * kSteps;
+  static_assert(kTopKKeys - VECTRA_SCAN_MAX_K >= kTopKRound, "room for a round of candidates");
   __shared__ uint64_t keys[kTopKKeys];
   __shared__ uint32_t fill;  // candidates in keys[k ..] since the last merge
   const int tid = static_cast<int>(threadIdx.x);
@@ -711,10 +710,10 @@ extern "C" int vectra_scan_top_k(const vectra_scan_top_k_args* a, hipStream_t st
   void* args[] = {&p};
   const bool wide = a->num_queries < kTopKWideBelow;
   const void* kernel = a->ids != nullptr
-                           ? (wide ? reinterpret_cast<const void*>(&scan_top_k_kernel<true, 1024>)
-                                   : reinterpret_cast<const void*>(&scan_top_k_kernel<true, 256>))
-                           : (wide ? reinterpret_cast<const void*>(&scan_top_k_kernel<false, 1024>)
-                                   : reinterpret_cast<const void*>(&scan_top_k_kernel<false, 256>));
+                           ? (wide ? reinterpret_cast<const void*>(&scan_top_k_kernel<true, 1024, 6, 1>)
+                                   : reinterpret_cast<const void*>(&scan_top_k_kernel<true, 256, 4, 4>))
+                           : (wide ? reinterpret_cast<const void*>(&scan_top_k_kernel<false, 1024, 6, 1>)
+                                   : reinterpret_cast<const void*>(&scan_top_k_kernel<false, 256, 4, 4>));
   return launched(hipLaunchKernel(kernel, dim3(static_cast<unsigned>(a->num_queries)), dim3(wide ? 1024 : 256), args,
                                   0, stream));
 }
