@@ -11,7 +11,9 @@ For bf16/fp16 inputs they compute, per (b, h) plane, in fp32:
   tile:  x_ij = fma(coef, q_i . k_j - |q_i|^2 / 2, c_j) - shift_i
   w = exp2(x); hi = 16-bit(w); lo = 16-bit(w - hi)   (bf16 round to nearest,
                                                       fp16 round toward zero)
-  total_i = sum_j (hi + lo);  acc_i = sum_j hi v_j + sum_j lo v_j
+  acc_i = sum_j hi v_j + sum_j lo v_j
+  total_i = sum_j w     (plane: the fp32 weights, added on the vector unit)
+  total_i = sum_j (hi + lo)   (tile: a product of ones on the matrix core)
   out_i = acc_i * (1 / total_i)
 
 with no clamp of the distance at 0 and no running maximum: shift_i = 0
@@ -98,14 +100,18 @@ def _weighted_fast(x, v16):
     return acc, total
 
 
-def _weighted(x, shift, v, kind):
-    """(acc [n, dv], total [n]) of logits x [n, nk] with per-row shifts."""
+def _weighted(x, shift, v, kind, sum_of_weights=False):
+    """(acc [n, dv], total [n]) of logits x [n, nk] with per-row shifts;
+    total sums the split weights hi + lo, or the fp32 weights themselves."""
     w = exp2_32((x - shift[:, None]).astype(F32) if shift is not None else x)
     hi, lo = split(w, kind)
     v64 = v.astype(np.float64)
     with np.errstate(invalid='ignore', over='ignore'):
         acc = (hi.astype(np.float64) @ v64 + lo.astype(np.float64) @ v64).astype(F32)
-        total = (hi.astype(np.float64) + lo.astype(np.float64)).sum(-1).astype(F32)
+        if sum_of_weights:
+            total = w.astype(np.float64).sum(-1).astype(F32)
+        else:
+            total = (hi.astype(np.float64) + lo.astype(np.float64)).sum(-1).astype(F32)
     return acc, total
 
 
@@ -145,11 +151,11 @@ def plane(q, k, v, gamma, bias, kind, one_pass=False):
     for b0 in range(0, nq, 16):
         rows = slice(b0, min(b0 + 16, nq))
         x0 = fma32(coef, s[rows], c[None, :])
-        acc, total = _weighted(x0, None, v, kind)
+        acc, total = _weighted(x0, None, v, kind, sum_of_weights=True)
         if not one_pass and not _in_range(total, kind).all():
             shift = _row_max(x0)
             x = fma32(coef, s[rows], (c[None, :] - shift[:, None]).astype(F32))
-            acc, total = _weighted(x, None, v, kind)
+            acc, total = _weighted(x, None, v, kind, sum_of_weights=True)
             path[rows] = SHIFTED
         out[rows] = _finish(acc, total)
     return out, path

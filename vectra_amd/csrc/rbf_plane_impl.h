@@ -15,10 +15,11 @@
 // 16t + 4g + r; those of key blocks 2p and 2p + 1 are the B operand of one
 // 16x16x32 step of the second product over keys read in the order
 // {32p + 4g .. +3, 32p + 16 + 4g .. +3}, and an odd last block takes a
-// 16x16x16 step.  K rows sit in LDS as loaded (the A operand of the first
-// product is row l % 16 of a key block, head dims 8g .. 8g+7, or 4g .. 4g+3
-// for 16-dim heads; read where it is used); V is written transposed; q goes
-// from HBM straight into the B operand.
+// 16x16x16 step.  K and V rows sit in LDS as loaded: the A operand of the
+// first product is row l % 16 of a key block, head dims 8g .. 8g+7 (4g ..
+// 4g+3 for 16-dim heads), read where it is used; that of the second is read
+// transposed from the V rows (ds_read_b64_tr_b16); q goes from HBM straight
+// into the B operand.
 //
 // Per-score arithmetic is one FMA, one exp2 and the 16-bit split of the
 // weight:
@@ -28,9 +29,10 @@
 //    and the per-query constant -gamma |q|^2 is left out (a softmax row does
 //    not see a shift), so the exp2 argument is one FMA of the product,
 //      x = 2 gamma log2(e) q.k + c_j = log2(e) (-gamma (d - |q|^2) + bias_j);
-//  * the softmax sum comes from the second product itself: a row of ones in
-//    the A operand sums the same hi + lo weights the values are weighted by,
-//    so the denominator needs no VALU add and no cross-lane reduction;
+//  * each lane adds up the fp32 weights it computes (keys 4g + r of every
+//    block), and the four lane groups of a query are summed at the end: two
+//    lane swaps, where a product of ones would take a quarter of the matrix
+//    instructions and eight more registers;
 //  * no running maximum is kept: if a query's weight sum leaves the range in
 //    which the 16-bit split is accurate and the value products cannot
 //    overflow (gamma < 0, a query far from every key, biases far from 0), its
@@ -43,6 +45,11 @@
 // the weight), as in rbf_mfma_kernel.  Keys past Nk have c_j = -inf, and
 // their K and V rows read as zeros, so they contribute nothing.  A fully masked
 // row ends as 0 * (1 / 0) = NaN, as eager softmax gives.
+//
+// Outputs leave as non-temporal stores of whole rows where the layout
+// allows: the plane's output is a quarter of its traffic, and written in
+// 32-byte pieces through the cache it cost HBM time in the middle of the
+// other workgroups' loads.
 //
 // Scheduling: one workgroup per plane, a wave per two query blocks (three
 // waves for 65 queries).  The waves share the staging of K and V and then
@@ -132,31 +139,22 @@ struct PlaneGeo {
   // K rows in LDS: an odd number of 16-byte units, so the 16 rows of one
   // operand read start in distinct bank groups.
   static constexpr int kKStride = kD * 2 + 16;
-  static constexpr int kKChunks = kKeys * kChunks;
-  // V^T rows: a multiple of 8 elements, an odd number of 16-byte units.
-  static constexpr int kVStride = kKeys + 8;
-  static constexpr int kPairKeys = 32 * (kNB / 2);  // keys read by 16x16x32 steps
-  static constexpr int kVPairSlots = kKeys / 2 * kChunks;
+  static constexpr int kKChunks = kKeys * kChunks;  // 16-byte pieces of K (and of V)
+  // V rows in LDS, in elements: 16 bytes of padding, as for K.
+  static constexpr int kVRow = kD + 8;
   static constexpr int kDTiles = kD / 16;
-  // Position of key j in a V^T row.  Below kPairKeys each 32-key group is
-  // stored as the 8-key runs {4g .. 4g+3, 16+4g .. 16+4g+3}, g = 0..3, so the
-  // A operand of a 16x16x32 step is one 16-byte read; the keys of an odd
-  // last block keep their order (8-byte reads of 4 keys).
-  static __device__ __forceinline__ int vt_pos(int j) {
-    return j >= kPairKeys ? j : (j & ~31) | (((j >> 2) & 3) << 3) | (((j >> 4) & 1) << 2) | (j & 3);
-  }
 };
 
 // Query blocks per wave: two, computed interleaved (their products share the
-// V^T operand reads, and each one's latencies are covered by the other's
+// K and V operand reads, and each one's latencies are covered by the other's
 // instructions).
 constexpr int kPlaneBlocksPerWave = 2;
 
-// 16-dim heads over at most 80 keys fit 8 waves per SIMD (64 VGPRs) with no
-// spills; more resident workgroups keep more of HBM's latency covered.
+// Tiles of at most 80 keys fit 8 waves per SIMD (64 VGPRs) with no spills;
+// more resident workgroups keep more of HBM's latency covered.
 template <typename T, typename OutT, int kD, int kKeys>
 __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2))
-__attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_plane_kernel(Problem p) {
+__attribute__((amdgpu_waves_per_eu(kKeys <= 80 ? 8 : 6))) void rbf_plane_kernel(Problem p) {
   using G = PlaneGeo<T, kD, kKeys>;
   using Ops = MfmaOps<T>;
   using Frag = typename G::Frag;
@@ -182,16 +180,22 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
   // over 80 keys of 32 dims); smaller workgroups loop for the rest.
   constexpr int kKRounds = 2;
 
-  __shared__ __align__(16) T vt_lds[kD * G::kVStride];
+  constexpr int kVRow = G::kVRow;
+  __shared__ __align__(16) T v_lds[kKeys * kVRow];  // V rows as loaded
   __shared__ __align__(16) char k_lds[kKeys * G::kKStride];
   __shared__ __align__(16) float c_lds[kKeys];  // folded key values
-  // Per key: whether it can contribute (not masked with a finite K row), and
-  // per key and 16-byte chunk of V, whether the chunk holds an inf or NaN.
-  __shared__ __align__(4) uint8_t k_live[kKeys];
-  __shared__ __align__(4) uint8_t v_bad[kKeys * kChunks];
+  // Per 16-key block: whether any of its keys can contribute (see below).
+  __shared__ __align__(8) uint8_t block_live[8];
+  static_assert(kNB <= 8, "one byte per key block");
 
+  args_in_sgprs(p.q, p.k, p.v, p.out, p.scale, p.bias, p.scale_dtype, p.bias_dtype, p.B, p.H, p.Nq, p.Nk);
+  args_in_sgprs(p.sq[0], p.sq[1], p.sq[2], p.sk[0], p.sk[1], p.sk[2], p.sv[0], p.sv[1], p.sv[2]);
+  args_in_sgprs(p.so[0], p.so[1], p.so[2], p.so[3], p.ssb, p.ssh, p.sbb, p.sbh, p.sbn, p.h_mul, p.h_shift);
   const int tid = static_cast<int>(threadIdx.x);
-  const int nthreads = static_cast<int>(blockDim.x);
+  // The launch's workgroup size, 64 threads per two query blocks (from Nq
+  // rather than blockDim.x, which would be one more dependent scalar load).
+  static_assert(kPer == 2, "two query blocks (32 rows) per wave");
+  const int nthreads = kWave * ((static_cast<int>(p.Nq) + 31) / 32);
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int col = lane & 15;
@@ -226,9 +230,9 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
   // Loads go through buffer resources whose extent ends at the last row of
   // the plane (rows past Nq or Nk read as zeros, a bounds check of the
   // hardware), with one per-lane offset computed once and per-round parts in
-  // scalar registers.  Piece i of K is row i / kChunks, 16-byte chunk
-  // i % kChunks; V pair slot i is rows 2 (i / kChunks) and + 1 of the same
-  // chunk.  No row offset reaches 2^32 (the host checks 144 rows of each stride).
+  // scalar registers.  Piece i of K (and of V) is row i / kChunks, 16-byte
+  // chunk i % kChunks.  No row offset reaches 2^32 (the host checks 144 rows
+  // of each stride).
   const char* kp = static_cast<const char*>(p.k) + (b * p.sk[0] + h * p.sk[1]) * 2;
   const char* vp = static_cast<const char*>(p.v) + (b * p.sv[0] + h * p.sv[1]) * 2;
   const char* qp = static_cast<const char*>(p.q) + (b * p.sq[0] + h * p.sq[1]) * 2;
@@ -238,12 +242,12 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
   const uint32_t chunk_off = static_cast<uint32_t>(lane % kChunks) * 16u;
   const uint32_t lane_rows = static_cast<uint32_t>(lane / kChunks);  // row of a piece within a round
   const uint32_t k_lane = lane_rows * k_row_bytes + chunk_off;
-  const uint32_t v_lane = 2u * lane_rows * v_row_bytes + chunk_off;
+  const uint32_t v_lane = lane_rows * v_row_bytes + chunk_off;
   constexpr int kRowsPerWave = kWave / kChunks;  // K rows (V row pairs) a wave covers per round
 
   // The coefficient and, per key, the folded value
   //   c_j = log2(e) (bias_j - gamma |k_j|^2)    (-inf past Nk)
-  // computed by the lane holding the first chunk of K row j.
+  // computed by the kChunks lanes holding K row j.
   const RawScalar scale_raw = load_raw_scalar(p.scale, b * p.ssb + h * p.ssh, p.scale_dtype);
   const char* const bp =
       has_bias ? static_cast<const char*>(p.bias) + (b * p.sbb + h * p.sbh) * bias_esize : nullptr;
@@ -261,26 +265,24 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
   auto k_piece = [&](int row0) {
     return load16_buf(k_rsrc, k_lane + static_cast<uint32_t>(row0) * k_row_bytes);
   };
-  auto v_pair = [&](int row0, uint4& r0, uint4& r1) {
-    const uint32_t off = v_lane + static_cast<uint32_t>(row0) * v_row_bytes;
-    r0 = load16_buf(v_rsrc, off);
-    r1 = load16_buf(v_rsrc, off + v_row_bytes);
+  auto v_piece = [&](int row0) {
+    return load16_buf(v_rsrc, v_lane + static_cast<uint32_t>(row0) * v_row_bytes);
   };
-  const int k_base = wave * kWave;  // first K piece (and V pair slot) of this wave
-  uint4 kr[kKRounds];
+  const int k_base = wave * kWave;  // first K and V piece of this wave
+  uint4 kr[kKRounds], vr[kKRounds];
   uint32_t bias_r[kKRounds];
 #pragma unroll
   for (int r = 0; r < kKRounds; ++r) {
     kr[r] = make_uint4(0, 0, 0, 0);
+    vr[r] = kr[r];
     bias_r[r] = 0;
     const int base = k_base + r * nthreads;
     if (base < G::kKChunks) {
       kr[r] = k_piece(base / kChunks);
       bias_r[r] = bias_of(base / kChunks);
+      vr[r] = v_piece(base / kChunks);
     }
   }
-  uint4 v0a = make_uint4(0, 0, 0, 0), v0b = v0a;
-  if (k_base < G::kVPairSlots) v_pair(2 * (k_base / kChunks), v0a, v0b);
   // This wave's query blocks: kPer * wave + j, j < blocks (1 or 2).
   const int first_block = kPer * wave;
   const int blocks = min(kPer, q_blocks - first_block);
@@ -292,118 +294,95 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
   const float coef = 2.f * kLog2e * decode_raw_scalar(scale_raw, p.scale_dtype);
   const float half_coef = -0.5f * coef;
 
-  // K into LDS as loaded, and each row's folded value (the kChunks lanes of
-  // a row are adjacent; every lane of a wave takes part in the reduction).
-  auto put_k = [&](int base, uint4 piece, uint32_t bias_raw) {
+  // One round of staging: K and V pieces base + lane (row base / kChunks +
+  // lane / kChunks, 16-byte chunk lane % kChunks) into LDS as loaded, each
+  // row's folded value, and whether the round's key blocks can contribute.
+  // Rows past Nk read as zeros (their weight is 0, and 0 * a non-finite
+  // value would not be).  A round covers whole 16-key blocks (one for
+  // 32-dim heads, two for 16-dim), and a block can be skipped if every key
+  // in it is masked (by its bias, or past Nk) with finite K and V rows: it
+  // gets weight exactly 0 from every finite query and adds exact zeros to
+  // every sum, bit for bit.
+  auto stage = [&](int base, uint4 kp_, uint4 vp_, uint32_t bias_raw) {
     const int row = base / kChunks + static_cast<int>(lane_rows);
-    const float sq = reduce_low<kChunks>(frag_norm<T>(piece), OpSum());
-    if (base + lane < G::kKChunks) {
-      *reinterpret_cast<uint4*>(k_lds + row * G::kKStride + static_cast<int>(chunk_off)) = piece;
-      if (chunk_off == 0) {
-        float x = 0.f;
-        if (has_bias) {
-          x = p.bias_dtype == VECTRA_F32    ? __uint_as_float(bias_raw)
-              : p.bias_dtype == VECTRA_BF16 ? __uint_as_float(bias_raw << 16)
-                                            : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bias_raw)));
-        }
-        const float c = row < n_k ? fmaf(half_coef, sq, x * kLog2e) : -INFINITY;
-        c_lds[row] = c;
-        // A key masked by its bias (or past Nk) whose K row is finite gets
-        // weight exactly 0 from every finite query.
-        k_live[row] = !(row >= n_k || (c == -INFINITY && __builtin_isfinite(sq)));
-      }
+    const bool in = G::kKChunks % kWave == 0 || base + lane < G::kKChunks;
+    const float sq = reduce_low<kChunks>(frag_norm<T>(kp_), OpSum());
+    float x = 0.f;
+    if (has_bias) {
+      x = p.bias_dtype == VECTRA_F32    ? __uint_as_float(bias_raw)
+          : p.bias_dtype == VECTRA_BF16 ? __uint_as_float(bias_raw << 16)
+                                        : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bias_raw)));
     }
-  };
-  // V^T: two keys of one value dim per 32-bit word (rows past Nk read as
-  // zeros: their weight is 0, and 0 * a non-finite value would not be).
-  auto put_v = [&](int i, uint4 r0, uint4 r1) {
-    const int row = 2 * (i / kChunks);
-    const int d0 = (i % kChunks) * 8;
+    const float c = row < n_k ? fmaf(half_coef, sq, x * kLog2e) : -INFINITY;
     // An all-ones exponent in either 16-bit half: (w & exp) + low carries
     // into that half's top bit, and into nothing else.
     constexpr uint32_t kExp = kBf16 ? 0x7f807f80u : 0x7c007c00u;
     constexpr uint32_t kLow = kBf16 ? 0x00800080u : 0x04000400u;
-    auto bad = [&](uint4 r) {
-      const uint32_t m = ((r.x & kExp) + kLow) | ((r.y & kExp) + kLow) | ((r.z & kExp) + kLow) | ((r.w & kExp) + kLow);
-      return static_cast<uint8_t>((m & 0x80008000u) != 0);
-    };
-    v_bad[row * kChunks + i % kChunks] = bad(r0);
-    v_bad[(row + 1) * kChunks + i % kChunks] = bad(r1);
-    const uint32_t w0[4] = {r0.x, r0.y, r0.z, r0.w};
-    const uint32_t w1[4] = {r1.x, r1.y, r1.z, r1.w};
-    T* dst = vt_lds + d0 * G::kVStride + G::vt_pos(row);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      // Elements 2e and 2e + 1 of the chunk, for keys row and row + 1.
-      *reinterpret_cast<uint32_t*>(dst + 2 * e * G::kVStride) = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u);
-      *reinterpret_cast<uint32_t*>(dst + (2 * e + 1) * G::kVStride) = __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u);
+    const uint32_t m = ((vp_.x & kExp) + kLow) | ((vp_.y & kExp) + kLow) | ((vp_.z & kExp) + kLow) |
+                       ((vp_.w & kExp) + kLow);
+    const bool v_bad = (m & 0x80008000u) != 0;
+    const bool live = in && ((row < n_k && !(c == -INFINITY && __builtin_isfinite(sq))) || v_bad);
+    const uint64_t mask = __builtin_amdgcn_ballot_w64(live);
+    if (in) {
+      *reinterpret_cast<uint4*>(k_lds + row * G::kKStride + static_cast<int>(chunk_off)) = kp_;
+      *reinterpret_cast<uint4*>(v_lds + row * kVRow + static_cast<int>(chunk_off / 2)) = vp_;
+      if (chunk_off == 0) c_lds[row] = c;
+    }
+    if (lane == 0) {
+      const int blk = base / kChunks / 16;
+      if constexpr (kChunks == 4) {
+        block_live[blk] = mask != 0;
+      } else {
+        static_assert(kChunks == 2, "16- or 32-dim heads");
+        block_live[blk] = static_cast<uint32_t>(mask) != 0;
+        if (blk + 1 < kNB) block_live[blk + 1] = (mask >> 32) != 0;
+      }
     }
   };
 #pragma unroll
   for (int r = 0; r < kKRounds; ++r) {
     const int base = k_base + r * nthreads;
-    if (base < G::kKChunks) put_k(base, kr[r], bias_r[r]);
+    if (base < G::kKChunks) stage(base, kr[r], vr[r], bias_r[r]);
   }
-  if (tid < G::kVPairSlots) put_v(tid, v0a, v0b);
   // Workgroups with fewer waves (fewer query blocks) stage the rest in
   // further rounds.
   for (int base = k_base + kKRounds * nthreads; base < G::kKChunks; base += nthreads)
-    put_k(base, k_piece(base / kChunks), bias_of(base / kChunks));
-  for (int base = k_base + nthreads; base < G::kVPairSlots; base += nthreads) {
-    uint4 r0, r1;
-    v_pair(2 * (base / kChunks), r0, r1);
-    if (base + lane < G::kVPairSlots) put_v(base + lane, r0, r1);
-  }
-  static_assert(kRowsPerWave * kChunks == kWave, "pieces of whole rows per wave");
+    stage(base, k_piece(base / kChunks), v_piece(base / kChunks), bias_of(base / kChunks));
+  static_assert(kRowsPerWave * kChunks == kWave && kRowsPerWave % 16 == 0, "pieces of whole key blocks per wave");
 
-  __syncthreads();  // K, the folded key values and V^T in place
+  __syncthreads();  // K, V, the folded key values and the live blocks in place
 
-  // 16-key blocks that can contribute: a block whose every key is masked
-  // with finite K and V rows adds exact zeros to every sum (bit for bit), so
-  // its products are skipped.  Bit t of live_blocks is block t (uniform).
-  auto key_live = [&](int j) -> bool {
-    if (j >= kKeys) return false;
-    uint32_t bad;
-    if constexpr (kChunks == 4) {
-      bad = *reinterpret_cast<const uint32_t*>(v_bad + 4 * j);
-    } else {
-      static_assert(kChunks == 2, "16- or 32-dim heads");
-      bad = *reinterpret_cast<const uint16_t*>(v_bad + 2 * j);
-    }
-    return k_live[j] != 0 || bad != 0;
-  };
-  const uint64_t live_lo = __builtin_amdgcn_ballot_w64(key_live(lane));
-  const uint64_t live_hi = kKeys > 64 ? __builtin_amdgcn_ballot_w64(key_live(lane + 64)) : 0;
+  // Bit t of live_blocks: key block t can contribute (uniform).
   uint32_t live_blocks = 0;
+  {
+    const uint2 bytes = *reinterpret_cast<const uint2*>(block_live);
 #pragma unroll
-  for (int t = 0; t < kNB; ++t)
-    if (((t < 4 ? live_lo >> (16 * t) : live_hi >> (16 * (t - 4))) & 0xffffu) != 0) live_blocks |= 1u << t;
-  live_blocks = __builtin_amdgcn_readfirstlane(live_blocks);
+    for (int t = 0; t < kNB; ++t)
+      live_blocks |= (((t < 4 ? bytes.x >> (8 * t) : bytes.y >> (8 * (t - 4))) & 1u) << t);
+    live_blocks = __builtin_amdgcn_readfirstlane(live_blocks);
+  }
 
   // Key block t's operand of the first product (read from LDS where it is
   // used rather than held across the pass, which would cost a wave slot).
   const char* const k_op = k_lds + col * G::kKStride + grp * kFragBytes;
   auto kc = [&](int t) { return *reinterpret_cast<const Frag*>(k_op + 16 * t * G::kKStride); };
 
-  const uint32_t one = Ops::kOnePair;
-  const Qk ones8 = __builtin_bit_cast(Qk, make_uint4(one, one, one, one));
-  const Pv ones4 = __builtin_bit_cast(Pv, make_uint2(one, one));
 
   // The wave's query blocks against every key of the plane.
   //
   // The logits are taken without the per-query constant -gamma |q|^2
   // (softmax does not see a per-row shift):
   //   x = 2 gamma log2(e) q.k + c_j = log2(e) (-gamma (d - |q|^2) + bias_j).
-  // exp2(x) is used unshifted unless the weights' sum, read off the ones
-  // product, leaves the range where the 16-bit split of the weights is
+  // exp2(x) is used unshifted unless the weights' sum leaves the range where the 16-bit split of the weights is
   // accurate and the value products cannot overflow; then the block is
   // computed once more with each query's exact maximum subtracted.
   f32x4 acc[kPer][G::kDTiles];
-  f32x4 total[kPer];
+  float total[kPer];  // this lane's share of a query's weight sum (keys 4g + r)
   // Weights of block t as packed 16-bit hi / lo pairs (keys 4g + 0,1 and 4g + 2,3).
-  auto weights = [&](const float (&xt)[4], uint32_t* hi, uint32_t* lo) {
+  auto weights = [&](const float (&xt)[4], uint32_t* hi, uint32_t* lo, float& sum) {
     const float w0 = __builtin_amdgcn_exp2f(xt[0]), w1 = __builtin_amdgcn_exp2f(xt[1]);
     const float w2 = __builtin_amdgcn_exp2f(xt[2]), w3 = __builtin_amdgcn_exp2f(xt[3]);
+    sum += (w0 + w1) + (w2 + w3);
     Ops::split2(w0, w1, hi[0], lo[0]);
     Ops::split2(w2, w3, hi[1], lo[1]);
   };
@@ -416,6 +395,11 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
     xt[2] = fmaf(coef, s[2], c.z - shift);
     xt[3] = fmaf(coef, s[3], c.w - shift);
   };
+  // A query's weight sum: the four lane groups hold keys 4g + r of every block.
+  auto reduce_totals = [&](auto n_tag) {
+#pragma unroll
+    for (int j = 0; j < decltype(n_tag)::value; ++j) total[j] = allreduce_bit32(allreduce_bit16(total[j], OpSum()), OpSum());
+  };
   // One pass over the keys for the first `n` query blocks, block pair by
   // block pair of keys, so only the logits of two key blocks per query
   // block are live at a time.
@@ -425,7 +409,7 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
     for (int j = 0; j < n; ++j) {
 #pragma unroll
       for (int u = 0; u < G::kDTiles; ++u) acc[j][u] = f32x4{0.f, 0.f, 0.f, 0.f};
-      total[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      total[j] = 0.f;
     }
 #pragma unroll
     for (int pp = 0; pp < kNB / 2; ++pp) {
@@ -437,55 +421,56 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
         logits(j, 2 * pp, shift[j], x0);
         logits(j, 2 * pp + 1, shift[j], x1);
         uint32_t hi[4], lo[4];
-        weights(x0, hi, lo);
-        weights(x1, hi + 2, lo + 2);
+        weights(x0, hi, lo, total[j]);
+        weights(x1, hi + 2, lo + 2, total[j]);
         p_hi[j] = __builtin_bit_cast(Qk, make_uint4(hi[0], hi[1], hi[2], hi[3]));
         p_lo[j] = __builtin_bit_cast(Qk, make_uint4(lo[0], lo[1], lo[2], lo[3]));
       }
 #pragma unroll
       for (int u = 0; u < G::kDTiles; ++u) {
-        const Qk a = *reinterpret_cast<const Qk*>(vt_lds + (16 * u + col) * G::kVStride + 32 * pp + 8 * grp);
+        // Lane (dim 16u + col, group g) gets keys 32pp + 4g + 0..3 and
+        // 32pp + 16 + 4g + 0..3 of that dim: within a group of 16 lanes,
+        // lane i addresses key row 32pp + 4g + i / 4 (+16), dims
+        // 16u + 4 (i % 4) .. +3.
+        const T* va = v_lds + (32 * pp + 4 * grp + col / 4) * kVRow + 16 * u + 4 * (col % 4);
+        const uint2 a0 = lds_read_tr16(va);
+        const uint2 a1 = lds_read_tr16(va + 16 * kVRow);
+        const Qk a = __builtin_bit_cast(Qk, make_uint4(a0.x, a0.y, a1.x, a1.y));
 #pragma unroll
         for (int j = 0; j < n; ++j) {
           acc[j][u] = Ops::qk(a, p_hi[j], acc[j][u]);
           acc[j][u] = Ops::qk(a, p_lo[j], acc[j][u]);
         }
       }
-#pragma unroll
-      for (int j = 0; j < n; ++j) {
-        total[j] = Ops::qk(ones8, p_hi[j], total[j]);
-        total[j] = Ops::qk(ones8, p_lo[j], total[j]);
-      }
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (kNB % 2 == 1) {
       constexpr int t = kNB - 1;
-      if (((live_blocks >> t) & 1u) == 0) return;
+      if (((live_blocks >> t) & 1u) == 0) {
+        reduce_totals(n_tag);
+        return;
+      }
       Pv p_hi[n], p_lo[n];
 #pragma unroll
       for (int j = 0; j < n; ++j) {
         float x0[4];
         logits(j, t, shift[j], x0);
         uint32_t hi[2], lo[2];
-        weights(x0, hi, lo);
+        weights(x0, hi, lo, total[j]);
         p_hi[j] = __builtin_bit_cast(Pv, make_uint2(hi[0], hi[1]));
         p_lo[j] = __builtin_bit_cast(Pv, make_uint2(lo[0], lo[1]));
       }
 #pragma unroll
       for (int u = 0; u < G::kDTiles; ++u) {
-        const Pv a = *reinterpret_cast<const Pv*>(vt_lds + (16 * u + col) * G::kVStride + 16 * t + 4 * grp);
+        const Pv a = __builtin_bit_cast(Pv, lds_read_tr16(v_lds + (16 * t + 4 * grp + col / 4) * kVRow + 16 * u + 4 * (col % 4)));
 #pragma unroll
         for (int j = 0; j < n; ++j) {
           acc[j][u] = Ops::pv(a, p_hi[j], acc[j][u]);
           acc[j][u] = Ops::pv(a, p_lo[j], acc[j][u]);
         }
       }
-#pragma unroll
-      for (int j = 0; j < n; ++j) {
-        total[j] = Ops::pv(ones4, p_hi[j], total[j]);
-        total[j] = Ops::pv(ones4, p_lo[j], total[j]);
-      }
     }
+    reduce_totals(n_tag);
   };
   // Each query's exact maximum logit in block j (the rare second pass).
   auto row_max = [&](int j) {
@@ -500,8 +485,8 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
     rmax = allreduce_bit32(allreduce_bit16(rmax, OpMax()), OpMax());
     return rmax == -INFINITY ? 0.f : rmax;  // every key masked: the row ends as NaN
   };
-  // Every row of the ones product holds the full sum of a query's weights.
-  // NaN (a NaN input) fails the test and is recomputed to NaN.  A block
+  // Every lane holds the full sum of its query's weights.  NaN (a NaN
+  // input) fails the test and is recomputed to NaN.  A block
   // that needs no shift is recomputed unshifted, to the same result.
   auto run = [&](auto n_tag) {
     constexpr int n = decltype(n_tag)::value;
@@ -510,7 +495,7 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
     bool again = false;
 #pragma unroll
     for (int j = 0; j < n; ++j) {
-      if (__builtin_amdgcn_ballot_w64(!(total[j][0] >= kSumLo && total[j][0] <= kSumHi))) {
+      if (__builtin_amdgcn_ballot_w64(!(total[j] >= kSumLo && total[j] <= kSumHi))) {
         shift[j] = row_max(j);
         again = true;
       }
@@ -524,12 +509,41 @@ __attribute__((amdgpu_waves_per_eu(kD == 16 && kKeys <= 80 ? 8 : 6))) void rbf_p
   }
 
   char* out_plane = static_cast<char*>(p.out) + (b * p.so[0] + h * p.so[1]) * static_cast<int64_t>(kOutSize);
+  if constexpr (kOutSize == 2 && G::kDTiles == 2) {
+    // 16-bit outputs of 32-dim heads, dense rows: whole rows per store.  A
+    // lane holds dims 16u + 4g .. +3 of its query (u = 0, 1); one swap
+    // between lane groups g = 2m and 2m + 1 leaves group g with dims
+    // 8t .. 8t + 7, t = 2 (g & 1) + g / 2, so each lane stores 16 bytes and
+    // a wave's store covers 16 whole rows.
+    if (out_vec && p.so[2] % 8 == 0 && p.so[1] % 8 == 0 && p.so[0] % 8 == 0) {
+      const uint32_t t = static_cast<uint32_t>(((grp & 1) << 1) | (grp >> 1));
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        if (j >= blocks) continue;
+        const float inv = __builtin_amdgcn_rcpf(total[j]);
+        uint32_t w[2][2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          w[u][0] = pack2<OutT>(acc[j][u][0] * inv, acc[j][u][1] * inv);
+          w[u][1] = pack2<OutT>(acc[j][u][2] * inv, acc[j][u][3] * inv);
+        }
+        const auto s0 = __builtin_amdgcn_permlane16_swap(w[0][0], w[1][0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(w[0][1], w[1][1], false, false);
+        const int32_t out_q = 16 * (first_block + j) + col;
+        if (out_q < n_q) {
+          const uint32_t off = (static_cast<uint32_t>(out_q) * o_row + 8u * t) * 2u;
+          __builtin_nontemporal_store(u32x4{s0[0], s1[0], s0[1], s1[1]}, reinterpret_cast<u32x4*>(out_plane + off));
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int32_t out_q = 16 * (first_block + j) + col;
     if (j < blocks && out_q < n_q) {
       // A fully masked row has sum 0 and ends as 0 * inf = NaN.
-      const float inv = __builtin_amdgcn_rcpf(total[j][0]);
+      const float inv = __builtin_amdgcn_rcpf(total[j]);
       const uint32_t row_off = static_cast<uint32_t>(out_q) * o_row;
 #pragma unroll
       for (int u = 0; u < G::kDTiles; ++u) {
