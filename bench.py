@@ -580,6 +580,15 @@ def main():
                                      'frac_of_peak': ceiling['GB/s'] / line_roof['peak'],
                                      'kernel_over_ceiling': achieved / ceiling['GB/s']}
         log(f'read ceiling: {ceiling["us"]:.2f} us, {ceiling["GB/s"]:.0f} GB/s')
+        # Where the output is a large share of the bytes (the plane kernels
+        # write a quarter), the same reads and writes streamed together.
+        out_bytes = shape.planes * shape.n_q * shape.value_dim * shape.element_bytes
+        if out_bytes * 10 >= fused:
+            mixed = read_ceiling.measure_read_write(fused - out_bytes, out_bytes)
+            line_roof['read_write_ceiling'] = {'us': mixed['us'], 'GB/s': mixed['GB/s'],
+                                               'frac_of_peak': mixed['GB/s'] / line_roof['peak'],
+                                               'kernel_over_ceiling': achieved / mixed['GB/s']}
+            log(f'read + write ceiling: {mixed["us"]:.2f} us, {mixed["GB/s"]:.0f} GB/s')
     line_roof['algorithmic_bytes'] = fused
 
     result = {

@@ -414,8 +414,10 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
       for (int u = 0; u < G::kDTiles; ++u) {
         const uint32_t off = (row_off + static_cast<uint32_t>(16 * u + 4 * grp) * o_dim) * 4u;
         const float ys[4] = {acc[j][u][0] * inv, acc[j][u][1] * inv, acc[j][u][2] * inv, acc[j][u][3] * inv};
+        // Non-temporal: the output is written once and not read back here.
         if (out_vec) {
-          *reinterpret_cast<float4*>(out_plane + off) = make_float4(ys[0], ys[1], ys[2], ys[3]);
+          __builtin_nontemporal_store(u32x4{__float_as_uint(ys[0]), __float_as_uint(ys[1]), __float_as_uint(ys[2]), __float_as_uint(ys[3])},
+                                      reinterpret_cast<u32x4*>(out_plane + off));
         } else {
 #pragma unroll
           for (int r = 0; r < 4; ++r) *reinterpret_cast<float*>(out_plane + off + r * o_dim * 4u) = ys[r];

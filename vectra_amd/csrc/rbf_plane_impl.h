@@ -46,7 +46,7 @@
 // their K and V rows read as zeros, so they contribute nothing.  A fully masked
 // row ends as 0 * (1 / 0) = NaN, as eager softmax gives.
 //
-// Outputs leave as non-temporal stores of whole rows where the layout
+// Outputs leave as non-temporal stores, of whole rows where the layout
 // allows: the plane's output is a quarter of its traffic, and written in
 // 32-byte pieces through the cache it cost HBM time in the middle of the
 // other workgroups' loads.
@@ -552,7 +552,8 @@ __attribute__((amdgpu_waves_per_eu(kKeys <= 80 ? 8 : 6))) void rbf_plane_kernel(
                     y3 = acc[j][u][3] * inv;
         if constexpr (kOutSize == 4) {
           if (out_vec) {
-            *reinterpret_cast<float4*>(out_plane + off) = make_float4(y0, y1, y2, y3);
+            __builtin_nontemporal_store(u32x4{__float_as_uint(y0), __float_as_uint(y1), __float_as_uint(y2), __float_as_uint(y3)},
+                                        reinterpret_cast<u32x4*>(out_plane + off));
           } else {
             const float ys[4] = {y0, y1, y2, y3};
 #pragma unroll
@@ -561,7 +562,8 @@ __attribute__((amdgpu_waves_per_eu(kKeys <= 80 ? 8 : 6))) void rbf_plane_kernel(
         } else {
           const uint32_t w01 = pack2<OutT>(y0, y1), w23 = pack2<OutT>(y2, y3);
           if (out_vec) {
-            *reinterpret_cast<uint2*>(out_plane + off) = make_uint2(w01, w23);
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            __builtin_nontemporal_store(u32x2{w01, w23}, reinterpret_cast<u32x2*>(out_plane + off));
           } else {
             const uint16_t hs[4] = {static_cast<uint16_t>(w01), static_cast<uint16_t>(w01 >> 16),
                                     static_cast<uint16_t>(w23), static_cast<uint16_t>(w23 >> 16)};
