@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VECTRA_SCAN_ABI_VERSION 2
+#define VECTRA_SCAN_ABI_VERSION 3
 
 /* Entries of a PQ sub-space's codebook (kPqCentroids,
  * include/vectra/index/simd_distance.h). */
@@ -174,6 +174,27 @@ typedef struct vectra_scan_top_k_args {
 } vectra_scan_top_k_args;
 
 int vectra_scan_top_k(const vectra_scan_top_k_args* args, hipStream_t stream);
+
+/*
+ * vectra_scan_top_k with a device workspace: below 64 queries the
+ * candidates of a query are cut into ranges, one workgroup each (at least 64
+ * candidates per range, at most 64 ranges, ranges * k <= 2048), and the
+ * workgroup that finishes last merges the ranges' k best; the results are
+ * the same bits as vectra_scan_top_k's.  The workspace is `workspace_bytes`
+ * of device memory, 256-byte aligned, whose first 256 bytes (arrival
+ * counters) are zero before the first call on it; every call leaves them
+ * zero.  With a NULL or smaller workspace than
+ * vectra_scan_top_k_workspace_bytes(args), or 64 queries or more, this is
+ * vectra_scan_top_k.  Calls that share a workspace must not overlap.
+ * Replaces the same reference loop as vectra_scan_top_k
+ * (shard_index.cc:236-264), for requests of one or a few queries.
+ */
+int vectra_scan_top_k_ws(const vectra_scan_top_k_args* args, void* workspace, int64_t workspace_bytes,
+                         hipStream_t stream);
+
+/* Workspace bytes vectra_scan_top_k_ws uses for these arguments (0: none;
+ * also 0 for arguments vectra_scan_top_k would reject). */
+int64_t vectra_scan_top_k_workspace_bytes(const vectra_scan_top_k_args* args);
 
 const char* vectra_scan_status_string(int status);
 int vectra_scan_abi_version(void);

@@ -27,7 +27,8 @@ def _declared_functions() -> set[str]:
 def test_library_exports_every_declared_symbol():
     declared = _declared_functions()
     assert declared == {'vectra_scan_rows', 'vectra_pq_distance_tables', 'vectra_scan_pq_adc',
-                        'vectra_scan_top_k', 'vectra_scan_status_string', 'vectra_scan_abi_version'}
+                        'vectra_scan_top_k', 'vectra_scan_top_k_ws', 'vectra_scan_top_k_workspace_bytes',
+                        'vectra_scan_status_string', 'vectra_scan_abi_version'}
     lib = ctypes.CDLL(_native.SCAN_LIBRARY)
     for name in declared:
         assert hasattr(lib, name), name
@@ -35,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _native.scan_library()
-    assert lib.vectra_scan_abi_version() == 2
+    assert lib.vectra_scan_abi_version() == 3
     assert lib.vectra_scan_status_string(0) == b'ok'
     assert lib.vectra_scan_status_string(1) == b'invalid argument'
     assert lib.vectra_scan_status_string(99) == b'unknown status'
@@ -177,8 +178,38 @@ def _top_k_args(**over):
 ])
 def test_top_k_arguments(over, status):
     lib = _native.scan_library()
-    assert lib.vectra_scan_top_k(ctypes.byref(_top_k_args(**over)), None) == status
+    args = ctypes.byref(_top_k_args(**over))
+    assert lib.vectra_scan_top_k(args, None) == status
+    assert lib.vectra_scan_top_k_ws(args, None, 0, None) == status
+    if status != OK:
+        assert lib.vectra_scan_top_k_workspace_bytes(args) == 0
     assert lib.vectra_scan_top_k(None, None) == INVALID
+    assert lib.vectra_scan_top_k_ws(None, None, 0, None) == INVALID
+    assert lib.vectra_scan_top_k_workspace_bytes(None) == 0
+
+
+# (queries, candidates, k) -> ranges per query: below 64 queries, ranges of
+# at least 64 candidates, at most 64 of them, ranges * k within 2048 keys.
+@pytest.mark.parametrize('n_q,n_rows,k,splits', [
+    (1, 2048, 10, 32), (1, 100, 10, 2), (1, 64, 10, 1), (1, 65, 10, 2), (63, 2048, 10, 32), (64, 2048, 10, 1),
+    (1, 1 << 20, 10, 64), (3, 1 << 20, 100, 16), (2, 1 << 20, 1000, 2), (2, 1 << 20, 1024, 2), (1, 5000, 1, 64),
+    (0, 2048, 10, 1),
+])
+def test_top_k_workspace_bytes(n_q, n_rows, k, splits):
+    lib = _native.scan_library()
+    args = _top_k_args(num_queries=n_q, num_rows=n_rows, k=k, out_stride=k)
+    want = 0 if splits == 1 else 256 + n_q * splits * k * 8
+    assert lib.vectra_scan_top_k_workspace_bytes(ctypes.byref(args)) == want
+    # Candidates from an id list count the same way.
+    ids = _top_k_args(num_queries=n_q, num_rows=10, ids=FAKE, num_ids=n_rows, k=k, out_stride=k)
+    assert lib.vectra_scan_top_k_workspace_bytes(ctypes.byref(ids)) == want
+
+
+def test_top_k_workspace_must_be_aligned():
+    lib = _native.scan_library()
+    args = ctypes.byref(_top_k_args(num_queries=1, num_rows=2048))
+    # Refused before anything is launched.
+    assert lib.vectra_scan_top_k_ws(args, FAKE + 8, 1 << 20, None) == INVALID
 
 
 def test_wrappers_refuse_cpu_tensors():

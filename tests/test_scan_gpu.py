@@ -225,12 +225,15 @@ def test_empty_inputs():
 # Exhaustive k-nearest search (vectra_scan_top_k).
 
 def _check_nearest(query, rows, k, ids=None, msg=''):
-    """The kernel's (distances, nodes) against the oracle: nodes exactly,
-    distances bit for bit (NaN as NaN)."""
-    got_d, got_n = scan.nearest(_gpu(query), _gpu(rows), k, None if ids is None else _gpu(ids))
+    """Every entry point's (distances, nodes) against the oracle: nodes
+    exactly, distances bit for bit (NaN as NaN).  Below 64 queries the split
+    form spreads a query over several workgroups; the others keep one."""
     want_d, want_n = oracle.nearest(query, rows, k, ids)
-    np.testing.assert_array_equal(got_n.cpu().numpy(), want_n, err_msg=msg)
-    _same(got_d, want_d, msg)
+    for form in scan.TOP_K_FORMS:
+        print(f'  form={form}', flush=True)
+        got_d, got_n = scan.nearest(_gpu(query), _gpu(rows), k, None if ids is None else _gpu(ids), form=form)
+        np.testing.assert_array_equal(got_n.cpu().numpy(), want_n, err_msg=f'{msg} {form}')
+        _same(got_d, want_d, f'{msg} {form}')
 
 
 def test_nearest_equals_the_reference_outputs(golden):
@@ -298,6 +301,26 @@ def test_nearest_over_a_large_shard():
     q = rng.standard_normal((2, 128)).astype(np.float32)
     print('nearest over 200k rows', flush=True)
     _check_nearest(q, rows, 10, msg='200k rows')
+
+
+def test_split_workspace_is_reused_across_calls():
+    """One workspace over calls of different sizes: each call leaves its
+    arrival counters at zero, so the next one's merges start clean."""
+    rng = np.random.default_rng(17)
+    rows = rng.standard_normal((6000, 64)).astype(np.float32)
+    cases = [(5, 6000, 100), (1, 300, 10), (63, 2048, 7), (2, 6000, 1024), (1, 65, 1), (4, 4000, 33)]
+    args = [(rng.standard_normal((n_q, 64)).astype(np.float32), n, k) for n_q, n, k in cases]
+    need = max(scan.workspace_bytes(_gpu(q), _gpu(rows[:n]), k) for q, n, k in args)
+    assert need > 0
+    workspace = torch.zeros(need, dtype=torch.uint8, device='cuda')
+    for q, n, k in args:
+        print(f'workspace reuse: queries={q.shape[0]} rows={n} k={k}', flush=True)
+        got_d, got_n = scan.nearest(_gpu(q), _gpu(rows[:n]), k, workspace=workspace)
+        want_d, want_n = oracle.nearest(q, rows[:n], k)
+        np.testing.assert_array_equal(got_n.cpu().numpy(), want_n)
+        _same(got_d, want_d, f'rows={n} k={k}')
+        torch.cuda.synchronize()
+        assert not workspace[:256].any(), 'arrival counters left non-zero'
 
 
 def test_nearest_matches_the_row_scan_and_a_sort():

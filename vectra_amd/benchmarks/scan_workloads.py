@@ -110,6 +110,13 @@ def make_sets(w: Workload, seed: int = 0, device='cuda') -> list[dict]:
         for i in range(n_sets):
             sets.append({'queries': torch.randn(w.queries, w.dim, generator=gen).to(device),
                          'rows': base if i == 0 else base * (1.0 + i / 64)})
+        if w.kind == 'topk':
+            # The split form's workspace (zeroed once; each call leaves its
+            # counters zero), made before the timed region.
+            need = scan.workspace_bytes(sets[0]['queries'], sets[0]['rows'], w.k)
+            workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device=device)
+            for s in sets:
+                s['workspace'] = workspace
     elif w.kind == 'adc':
         base = torch.randint(0, 256, (w.count, w.subspaces), generator=gen, dtype=torch.uint8).to(device)
         for i in range(n_sets):
@@ -137,7 +144,7 @@ def launch(w: Workload, inputs: dict, out: torch.Tensor) -> torch.Tensor:
     if w.kind == 'rows':
         return scan.l2_squared_distances(inputs['queries'], inputs['rows'], out=out)
     if w.kind == 'topk':
-        return scan.nearest(inputs['queries'], inputs['rows'], w.k, out=out)
+        return scan.nearest(inputs['queries'], inputs['rows'], w.k, out=out, workspace=inputs.get('workspace'))
     if w.kind == 'adc':
         return scan.pq_adc_distances(inputs['tables'], inputs['codes'], out=out)
     return scan.pq_distance_tables(inputs['queries'], inputs['codebooks'], w.subspaces, out=out)

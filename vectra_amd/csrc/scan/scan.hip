@@ -38,6 +38,7 @@
 #include <math.h>
 #include <stdint.h>
 
+
 #include "vectra_scan.h"
 
 namespace vectra_scan {
@@ -398,8 +399,17 @@ int launch_rows(RowScan& p, hipStream_t stream) {
 // that unsigned order follows float order, above the node id.  The workgroup
 // holds the k best keys and the candidates that beat the k-th since the last
 // merge in LDS; when those could overflow the buffer, and at the end, the
-// keys are sorted (bitonic) and the first k kept.  No device memory besides
-// the inputs and outputs.
+// keys are sorted (bitonic) and the first k kept.
+//
+// Split form (few queries): a query's candidates are cut into `splits`
+// contiguous ranges, one workgroup each; a workgroup writes the k best keys
+// of its range to device memory and counts itself in the query's arrival
+// counter, and the workgroup that arrives last gathers the splits * k keys
+// (at most the LDS buffer), sorts them and writes the result.  The k nearest
+// of the whole list are among the union of every range's k nearest, and
+// keys are unique per (distance, node, position), so the result is the one
+// workgroup form's, bit for bit.  The last workgroup puts the counter back to
+// zero, so the counters are zero between calls.
 struct TopK {
   const float* queries;
   const float* rows;
@@ -409,6 +419,10 @@ struct TopK {
   int64_t query_stride, row_stride, out_stride;
   int64_t num_rows, num_cand;
   int32_t dim, k;
+  int32_t splits;     // workgroups per query (1: no split)
+  int64_t split_len;  // candidates per split (the last one may have fewer)
+  uint64_t* partial;  // [queries][splits][k] keys of each split's k best
+  uint32_t* arrived;  // [queries] splits done; zero between calls
 };
 
 constexpr int kTopKKeys = 2048;        // LDS keys: the k best, then the new candidates
@@ -441,10 +455,14 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
   static_assert(kTopKKeys - VECTRA_SCAN_MAX_K >= kTopKRound, "room for a round of candidates");
   __shared__ uint64_t keys[kTopKKeys];
   __shared__ uint32_t fill;  // candidates in keys[k ..] since the last merge
+  __shared__ uint32_t last;  // split form: this workgroup is the query's last
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & (kLanes - 1);
   const int group = tid / kLanes;
-  const int64_t q = blockIdx.x;
+  const int64_t q = blockIdx.x / p.splits;
+  const int split = static_cast<int>(blockIdx.x - q * p.splits);
+  const int64_t cand_begin = split * p.split_len;
+  const int64_t cand_end = cand_begin + p.split_len < p.num_cand ? cand_begin + p.split_len : p.num_cand;
   const int k = p.k;
   const int full = p.dim - p.dim % kLanes;
   const int tail = p.dim - full;
@@ -478,7 +496,7 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
   };
 
   uint64_t worst = kNoKey;  // the k-th best key so far; empty while fewer than k
-  for (int64_t base = 0; base < p.num_cand; base += kTopKRound) {
+  for (int64_t base = cand_begin; base < cand_end; base += kTopKRound) {
     // A round: kSteps steps of kTopKCands candidates per 16-lane group, a
     // step's loads issued before any of its sums (each candidate's own
     // operations keep the row scan's order).
@@ -489,7 +507,7 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
 #pragma unroll
       for (int c = 0; c < kTopKCands; ++c) {
         const int64_t cand = base + static_cast<int64_t>(s * kTopKCands + c) * kTopKGroups + group;
-        valid[c] = cand < p.num_cand;
+        valid[c] = cand < cand_end;
         row[c] = valid[c] ? cand : 0;
         if constexpr (kIds) {
           const uint32_t id = valid[c] ? p.ids[cand] : 0u;
@@ -551,6 +569,27 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
   }
   const int n = static_cast<int>(fill);
   if (n > 0) merge(n);
+  if (p.splits > 1) {
+    // This range's k best to device memory, visible device-wide before the
+    // arrival is counted: the barrier completes every wave's stores to this
+    // XCD's L2, and one release at agent scope writes them back (the
+    // workgroup that reads them may sit on another XCD, behind another L2).
+    uint64_t* part = p.partial + (q * p.splits + split) * k;
+    for (int r = tid; r < k; r += kTopKThreads) part[r] = keys[r];
+    __syncthreads();
+    if (tid == 0) {
+      __threadfence();
+      last = atomicAdd(&p.arrived[q], 1u) == static_cast<uint32_t>(p.splits - 1);
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();  // acquire: the other ranges' keys
+    const int all = p.splits * k;
+    const uint64_t* parts = p.partial + q * p.splits * k;
+    for (int i = tid; i < all; i += kTopKThreads) keys[i] = parts[i];
+    merge(all - k);
+    if (tid == 0) p.arrived[q] = 0u;
+  }
   for (int r = tid; r < k; r += kTopKThreads) {
     const uint64_t key = keys[r];
     const int64_t off = q * p.out_stride + r;
@@ -676,25 +715,38 @@ extern "C" int vectra_scan_pq_adc(const vectra_pq_adc_args* a, hipStream_t strea
       hipLaunchKernel(reinterpret_cast<const void*>(&pq_adc_kernel<false>), grid, dim3(kThreads), args, 0, stream));
 }
 
-extern "C" int vectra_scan_top_k(const vectra_scan_top_k_args* a, hipStream_t stream) {
+namespace {
+
+// Split form: below kSplitBelow queries, a query's candidates are cut into
+// ranges of at least kSplitCands (one step of the 4-wave kernel) over at
+// most kSplitMax workgroups, and splits * k keys must fit the LDS buffer of
+// the workgroup that merges them.
+constexpr int64_t kSplitBelow = 64;
+constexpr int64_t kSplitCands = 64;
+constexpr int64_t kSplitMax = 64;
+constexpr int64_t kCounterBytes = 256;  // the arrival counters' block (kSplitBelow of them)
+static_assert(kSplitBelow * 4 <= kCounterBytes, "counters of every query of the split form");
+
+// Validates the arguments and fills the kernel parameters (splits = 1).
+int top_k_params(const vectra_scan_top_k_args* a, TopK& p) {
   if (a == nullptr) return VECTRA_SCAN_INVALID_ARGUMENT;
   if (a->dimension < 0 || a->num_queries < 0 || a->num_rows < 0 || (a->ids != nullptr && a->num_ids < 0))
     return VECTRA_SCAN_INVALID_ARGUMENT;
   if (a->k < 1 || a->k > VECTRA_SCAN_MAX_K) return VECTRA_SCAN_INVALID_ARGUMENT;
   if (a->row_stride < a->dimension || a->query_stride < a->dimension || a->out_stride < a->k)
     return VECTRA_SCAN_INVALID_ARGUMENT;
-  if (a->num_queries == 0) return VECTRA_SCAN_OK;
   const int64_t cand = a->ids != nullptr ? a->num_ids : a->num_rows;
-  const bool reads = a->dimension > 0 && cand > 0;
-  if (a->distances == nullptr || a->nodes == nullptr || (reads && (a->queries == nullptr || a->rows == nullptr)))
-    return VECTRA_SCAN_INVALID_ARGUMENT;
-  // Node ids are 32-bit, below VECTRA_SCAN_NO_NODE; one workgroup per query.
-  if (a->num_rows > int64_t{VECTRA_SCAN_NO_NODE} || a->num_queries > 0x7fffffffLL) return VECTRA_SCAN_TOO_LARGE;
-  const int64_t lim = int64_t{1} << 62;
-  if ((a->num_rows > 0 && a->row_stride > lim / a->num_rows) || a->out_stride > lim / a->num_queries ||
-      a->query_stride > lim / a->num_queries)
-    return VECTRA_SCAN_TOO_LARGE;
-  TopK p;
+  if (a->num_queries > 0) {
+    const bool reads = a->dimension > 0 && cand > 0;
+    if (a->distances == nullptr || a->nodes == nullptr || (reads && (a->queries == nullptr || a->rows == nullptr)))
+      return VECTRA_SCAN_INVALID_ARGUMENT;
+    // Node ids are 32-bit, below VECTRA_SCAN_NO_NODE; one workgroup per query.
+    if (a->num_rows > int64_t{VECTRA_SCAN_NO_NODE} || a->num_queries > 0x7fffffffLL) return VECTRA_SCAN_TOO_LARGE;
+    const int64_t lim = int64_t{1} << 62;
+    if ((a->num_rows > 0 && a->row_stride > lim / a->num_rows) || a->out_stride > lim / a->num_queries ||
+        a->query_stride > lim / a->num_queries)
+      return VECTRA_SCAN_TOO_LARGE;
+  }
   p.queries = a->queries;
   p.rows = a->rows;
   p.ids = a->ids;
@@ -707,15 +759,82 @@ extern "C" int vectra_scan_top_k(const vectra_scan_top_k_args* a, hipStream_t st
   p.num_cand = cand;
   p.dim = a->dimension;
   p.k = a->k;
+  p.splits = 1;
+  p.split_len = cand;
+  p.partial = nullptr;
+  p.arrived = nullptr;
+  return VECTRA_SCAN_OK;
+}
+
+// Workgroups per query of the split form for valid parameters (1: none).
+int64_t top_k_splits(int64_t queries, const TopK& p) {
+  if (queries < 1 || queries >= kSplitBelow) return 1;
+  int64_t kp = 1;
+  while (kp < p.k) kp <<= 1;
+  int64_t s = kTopKKeys / kp;
+  if (s > kSplitMax) s = kSplitMax;
+  const int64_t by_cands = (p.num_cand + kSplitCands - 1) / kSplitCands;
+  if (s > by_cands) s = by_cands;
+  return s >= 2 ? s : 1;
+}
+
+// Workspace bytes of the split form: the counter block, then the keys.
+int64_t top_k_workspace(int64_t queries, int64_t splits, int k) {
+  return splits > 1 ? kCounterBytes + queries * splits * k * int64_t{8} : 0;
+}
+
+int launch_top_k(int64_t queries, TopK& p, hipStream_t stream) {
   void* args[] = {&p};
-  const bool wide = a->num_queries < kTopKWideBelow;
-  const void* kernel = a->ids != nullptr
+  if (p.splits > 1) {
+    const void* kernel = p.ids != nullptr ? reinterpret_cast<const void*>(&scan_top_k_kernel<true, 256, 4, 1>)
+                                          : reinterpret_cast<const void*>(&scan_top_k_kernel<false, 256, 4, 1>);
+    return launched(hipLaunchKernel(kernel, dim3(static_cast<unsigned>(queries * p.splits)), dim3(256), args, 0,
+                                    stream));
+  }
+  const bool wide = queries < kTopKWideBelow;
+  const void* kernel = p.ids != nullptr
                            ? (wide ? reinterpret_cast<const void*>(&scan_top_k_kernel<true, 1024, 6, 1>)
                                    : reinterpret_cast<const void*>(&scan_top_k_kernel<true, 256, 4, 4>))
                            : (wide ? reinterpret_cast<const void*>(&scan_top_k_kernel<false, 1024, 6, 1>)
                                    : reinterpret_cast<const void*>(&scan_top_k_kernel<false, 256, 4, 4>));
-  return launched(hipLaunchKernel(kernel, dim3(static_cast<unsigned>(a->num_queries)), dim3(wide ? 1024 : 256), args,
-                                  0, stream));
+  return launched(hipLaunchKernel(kernel, dim3(static_cast<unsigned>(queries)), dim3(wide ? 1024 : 256), args, 0,
+                                  stream));
+}
+
+// Points the split form at a workspace: counters first, keys after.
+void use_workspace(TopK& p, int64_t splits, void* base) {
+  p.splits = static_cast<int32_t>(splits);
+  p.split_len = (p.num_cand + splits - 1) / splits;
+  p.arrived = static_cast<uint32_t*>(base);
+  p.partial = reinterpret_cast<uint64_t*>(static_cast<char*>(base) + kCounterBytes);
+}
+
+}  // namespace
+
+extern "C" int vectra_scan_top_k(const vectra_scan_top_k_args* a, hipStream_t stream) {
+  TopK p;
+  const int st = top_k_params(a, p);
+  if (st != VECTRA_SCAN_OK || a->num_queries == 0) return st;
+  return launch_top_k(a->num_queries, p, stream);
+}
+
+extern "C" int64_t vectra_scan_top_k_workspace_bytes(const vectra_scan_top_k_args* a) {
+  TopK p;
+  if (top_k_params(a, p) != VECTRA_SCAN_OK) return 0;
+  return top_k_workspace(a->num_queries, top_k_splits(a->num_queries, p), p.k);
+}
+
+extern "C" int vectra_scan_top_k_ws(const vectra_scan_top_k_args* a, void* workspace, int64_t workspace_bytes,
+                                    hipStream_t stream) {
+  TopK p;
+  const int st = top_k_params(a, p);
+  if (st != VECTRA_SCAN_OK || a->num_queries == 0) return st;
+  if (workspace != nullptr && (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return VECTRA_SCAN_INVALID_ARGUMENT;
+  const int64_t splits = top_k_splits(a->num_queries, p);
+  if (splits > 1 && workspace != nullptr && workspace_bytes >= top_k_workspace(a->num_queries, splits, p.k))
+    use_workspace(p, splits, workspace);
+  return launch_top_k(a->num_queries, p, stream);
 }
 
 extern "C" const char* vectra_scan_status_string(int status) {

@@ -220,14 +220,7 @@ def pq_adc_distances(tables: torch.Tensor, codes: torch.Tensor, ids=None, out=No
     return out
 
 
-def nearest(queries: torch.Tensor, rows: torch.Tensor, k: int, ids=None, out=None):
-    """ExhaustiveSearch for each query: (distances [num_queries, k] float32,
-    nodes [num_queries, k] uint32), nearest first by (distance, node id).
-
-    Candidates are rows ids[i] (ids not below the row count are skipped,
-    duplicates kept) or every row; slots past the number of candidates hold
-    +inf and NO_NODE.  k is 1 .. MAX_K.  `out` may give the two output
-    tensors (contiguous, of those shapes and dtypes)."""
+def _top_k_args(queries, rows, k, ids, out):
     queries = _matrix(queries, 'queries', torch.float32)
     rows = _matrix(rows, 'rows', torch.float32)
     if queries.shape[1] != rows.shape[1]:
@@ -249,6 +242,51 @@ def nearest(queries: torch.Tensor, rows: torch.Tensor, k: int, ids=None, out=Non
                      rows.data_ptr(), rows.shape[0], _row_stride(rows),
                      None if ids is None else ids.data_ptr(), 0 if ids is None else ids.shape[0],
                      distances.data_ptr(), nodes.data_ptr(), k)
-    with torch.cuda.device(rows.device):
-        _check(_native.scan_library().vectra_scan_top_k(ctypes.byref(args), _stream(rows.device)))
+    # The tensors the arguments point into stay referenced with them.
+    return args, (queries, rows, ids), distances, nodes
+
+
+TOP_K_FORMS = ('split', 'single')
+
+
+def workspace_bytes(queries: torch.Tensor, rows: torch.Tensor, k: int, ids=None) -> int:
+    """Device workspace bytes nearest(form='split') uses for these inputs
+    (vectra_scan_top_k_workspace_bytes; 0: none)."""
+    args, _keep, _d, _n = _top_k_args(queries, rows, k, ids, None)
+    return int(_native.scan_library().vectra_scan_top_k_workspace_bytes(ctypes.byref(args)))
+
+
+def nearest(queries: torch.Tensor, rows: torch.Tensor, k: int, ids=None, out=None, form='split', workspace=None):
+    """ExhaustiveSearch for each query: (distances [num_queries, k] float32,
+    nodes [num_queries, k] uint32), nearest first by (distance, node id).
+
+    Candidates are rows ids[i] (ids not below the row count are skipped,
+    duplicates kept) or every row; slots past the number of candidates hold
+    +inf and NO_NODE.  k is 1 .. MAX_K.  `out` may give the two output
+    tensors (contiguous, of those shapes and dtypes).
+
+    `form` picks the entry point, all with the same results: 'split'
+    (vectra_scan_top_k_ws: below 64 queries a query's candidates are spread
+    over several workgroups; `workspace` is a uint8 CUDA tensor of at least
+    workspace_bytes(...) whose first 256 bytes are zero before its first use,
+    or None to allocate a zeroed one) or 'single' (vectra_scan_top_k, one
+    workgroup per query)."""
+    if form not in TOP_K_FORMS:
+        raise ValueError(f'form must be one of {TOP_K_FORMS}')
+    args, _keep, distances, nodes = _top_k_args(queries, rows, k, ids, out)
+    lib = _native.scan_library()
+    device = distances.device
+    with torch.cuda.device(device):
+        stream = _stream(device)
+        if form == 'single':
+            _check(lib.vectra_scan_top_k(ctypes.byref(args), stream))
+        else:
+            need = int(lib.vectra_scan_top_k_workspace_bytes(ctypes.byref(args)))
+            if workspace is None:
+                workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device=device)
+            _on_gpu(workspace, 'workspace')
+            if workspace.dtype != torch.uint8 or not workspace.is_contiguous():
+                raise ValueError('workspace must be a contiguous uint8 tensor')
+            _check(lib.vectra_scan_top_k_ws(ctypes.byref(args), ctypes.c_void_p(workspace.data_ptr()),
+                                            workspace.numel(), stream))
     return distances, nodes

@@ -81,6 +81,10 @@ def scan_library() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         fn.restype = ctypes.c_int
+    lib.vectra_scan_top_k_ws.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    lib.vectra_scan_top_k_ws.restype = ctypes.c_int
+    lib.vectra_scan_top_k_workspace_bytes.argtypes = [ctypes.c_void_p]
+    lib.vectra_scan_top_k_workspace_bytes.restype = ctypes.c_int64
     lib.vectra_scan_status_string.argtypes = [ctypes.c_int]
     lib.vectra_scan_status_string.restype = ctypes.c_char_p
     lib.vectra_scan_abi_version.argtypes = []
