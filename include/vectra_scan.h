@@ -19,7 +19,8 @@
  *
  * Contract shared by every entry point:
  *  - all pointers are device pointers the caller owns; the library allocates
- *    nothing and keeps no state between calls;
+ *    nothing and keeps no state between calls (vectra_scan_top_k_no_alloc
+ *    keeps a static scratch array per GPU, zero between calls);
  *  - work is queued on `stream`, asynchronously; nothing is synchronised;
  *  - sizes and strides are in elements (floats, or bytes for codes);
  *  - zero counts are valid and launch nothing;
@@ -195,6 +196,18 @@ int vectra_scan_top_k_ws(const vectra_scan_top_k_args* args, void* workspace, in
 /* Workspace bytes vectra_scan_top_k_ws uses for these arguments (0: none;
  * also 0 for arguments vectra_scan_top_k would reject). */
 int64_t vectra_scan_top_k_workspace_bytes(const vectra_scan_top_k_args* args);
+
+/*
+ * vectra_scan_top_k_ws with the library's own scratch instead of a
+ * workspace: it allocates nothing, for callers that cannot allocate (code
+ * under HIP graph capture, serving loops that forbid allocation).  No
+ * counterpart in the reference.  The scratch is a static device array of
+ * 1,048,832 bytes on each GPU the library runs on, held until the process
+ * ends; a call whose split form would need more returns
+ * VECTRA_SCAN_TOO_LARGE (none does within the limits above).  Every call on
+ * one GPU shares that GPU's scratch: calls that overlap on one GPU race.
+ */
+int vectra_scan_top_k_no_alloc(const vectra_scan_top_k_args* args, hipStream_t stream);
 
 const char* vectra_scan_status_string(int status);
 int vectra_scan_abi_version(void);

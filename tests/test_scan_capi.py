@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     declared = _declared_functions()
     assert declared == {'vectra_scan_rows', 'vectra_pq_distance_tables', 'vectra_scan_pq_adc',
                         'vectra_scan_top_k', 'vectra_scan_top_k_ws', 'vectra_scan_top_k_workspace_bytes',
-                        'vectra_scan_status_string', 'vectra_scan_abi_version'}
+                        'vectra_scan_top_k_no_alloc', 'vectra_scan_status_string', 'vectra_scan_abi_version'}
     lib = ctypes.CDLL(_native.SCAN_LIBRARY)
     for name in declared:
         assert hasattr(lib, name), name
@@ -181,10 +181,12 @@ def test_top_k_arguments(over, status):
     args = ctypes.byref(_top_k_args(**over))
     assert lib.vectra_scan_top_k(args, None) == status
     assert lib.vectra_scan_top_k_ws(args, None, 0, None) == status
+    assert lib.vectra_scan_top_k_no_alloc(args, None) == status
     if status != OK:
         assert lib.vectra_scan_top_k_workspace_bytes(args) == 0
     assert lib.vectra_scan_top_k(None, None) == INVALID
     assert lib.vectra_scan_top_k_ws(None, None, 0, None) == INVALID
+    assert lib.vectra_scan_top_k_no_alloc(None, None) == INVALID
     assert lib.vectra_scan_top_k_workspace_bytes(None) == 0
 
 
@@ -200,6 +202,8 @@ def test_top_k_workspace_bytes(n_q, n_rows, k, splits):
     args = _top_k_args(num_queries=n_q, num_rows=n_rows, k=k, out_stride=k)
     want = 0 if splits == 1 else 256 + n_q * splits * k * 8
     assert lib.vectra_scan_top_k_workspace_bytes(ctypes.byref(args)) == want
+    # The library's own scratch holds the largest of them (63 queries of 2048 keys).
+    assert want <= 256 + 64 * 2048 * 8
     # Candidates from an id list count the same way.
     ids = _top_k_args(num_queries=n_q, num_rows=10, ids=FAKE, num_ids=n_rows, k=k, out_stride=k)
     assert lib.vectra_scan_top_k_workspace_bytes(ctypes.byref(ids)) == want

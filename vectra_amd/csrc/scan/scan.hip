@@ -38,6 +38,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
 
 #include "vectra_scan.h"
 
@@ -715,6 +716,14 @@ extern "C" int vectra_scan_pq_adc(const vectra_pq_adc_args* a, hipStream_t strea
       hipLaunchKernel(reinterpret_cast<const void*>(&pq_adc_kernel<false>), grid, dim3(kThreads), args, 0, stream));
 }
 
+// The scratch of vectra_scan_top_k_no_alloc: room for the largest workspace
+// of the split form (fewer than kSplitBelow queries of at most kTopKKeys
+// keys each, after the counter block), one copy per GPU for the life of the
+// process.  Zero when the library is loaded; every call leaves its counters
+// zero again.
+constexpr int64_t kNoAllocScratchBytes = 256 + 64 * 2048 * 8;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 namespace {
 
 // Split form: below kSplitBelow queries, a query's candidates are cut into
@@ -726,6 +735,7 @@ constexpr int64_t kSplitCands = 64;
 constexpr int64_t kSplitMax = 64;
 constexpr int64_t kCounterBytes = 256;  // the arrival counters' block (kSplitBelow of them)
 static_assert(kSplitBelow * 4 <= kCounterBytes, "counters of every query of the split form");
+static_assert(kNoAllocScratchBytes == kCounterBytes + kSplitBelow * kTopKKeys * 8, "the scratch's size");
 
 // Validates the arguments and fills the kernel parameters (splits = 1).
 int top_k_params(const vectra_scan_top_k_args* a, TopK& p) {
@@ -809,6 +819,24 @@ void use_workspace(TopK& p, int64_t splits, void* base) {
   p.partial = reinterpret_cast<uint64_t*>(static_cast<char*>(base) + kCounterBytes);
 }
 
+// Device address of `scratch` on each device, resolved on the entry point's
+// first call there (the array's host-side name is not a device address).
+constexpr int kMaxDevices = 64;
+std::atomic<void*> scratch_ptr[kMaxDevices];
+
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return VECTRA_SCAN_LAUNCH_FAILED;
+  void* ptr = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr)
+      return VECTRA_SCAN_LAUNCH_FAILED;
+    scratch_ptr[dev].store(ptr, std::memory_order_release);
+  }
+  *out = ptr;
+  return VECTRA_SCAN_OK;
+}
+
 }  // namespace
 
 extern "C" int vectra_scan_top_k(const vectra_scan_top_k_args* a, hipStream_t stream) {
@@ -834,6 +862,21 @@ extern "C" int vectra_scan_top_k_ws(const vectra_scan_top_k_args* a, void* works
   const int64_t splits = top_k_splits(a->num_queries, p);
   if (splits > 1 && workspace != nullptr && workspace_bytes >= top_k_workspace(a->num_queries, splits, p.k))
     use_workspace(p, splits, workspace);
+  return launch_top_k(a->num_queries, p, stream);
+}
+
+extern "C" int vectra_scan_top_k_no_alloc(const vectra_scan_top_k_args* a, hipStream_t stream) {
+  TopK p;
+  const int st = top_k_params(a, p);
+  if (st != VECTRA_SCAN_OK || a->num_queries == 0) return st;
+  const int64_t splits = top_k_splits(a->num_queries, p);
+  if (splits > 1) {
+    if (top_k_workspace(a->num_queries, splits, p.k) > kNoAllocScratchBytes) return VECTRA_SCAN_TOO_LARGE;
+    void* base = nullptr;
+    const int sa = scratch_address(&base);
+    if (sa != VECTRA_SCAN_OK) return sa;
+    use_workspace(p, splits, base);
+  }
   return launch_top_k(a->num_queries, p, stream);
 }
 

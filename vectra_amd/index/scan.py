@@ -246,7 +246,7 @@ def _top_k_args(queries, rows, k, ids, out):
     return args, (queries, rows, ids), distances, nodes
 
 
-TOP_K_FORMS = ('split', 'single')
+TOP_K_FORMS = ('split', 'single', 'no_alloc')
 
 
 def workspace_bytes(queries: torch.Tensor, rows: torch.Tensor, k: int, ids=None) -> int:
@@ -269,8 +269,9 @@ def nearest(queries: torch.Tensor, rows: torch.Tensor, k: int, ids=None, out=Non
     (vectra_scan_top_k_ws: below 64 queries a query's candidates are spread
     over several workgroups; `workspace` is a uint8 CUDA tensor of at least
     workspace_bytes(...) whose first 256 bytes are zero before its first use,
-    or None to allocate a zeroed one) or 'single' (vectra_scan_top_k, one
-    workgroup per query)."""
+    or None to allocate a zeroed one), 'single' (vectra_scan_top_k, one
+    workgroup per query) or 'no_alloc' (vectra_scan_top_k_no_alloc, the
+    split form on the library's own scratch)."""
     if form not in TOP_K_FORMS:
         raise ValueError(f'form must be one of {TOP_K_FORMS}')
     args, _keep, distances, nodes = _top_k_args(queries, rows, k, ids, out)
@@ -280,6 +281,8 @@ def nearest(queries: torch.Tensor, rows: torch.Tensor, k: int, ids=None, out=Non
         stream = _stream(device)
         if form == 'single':
             _check(lib.vectra_scan_top_k(ctypes.byref(args), stream))
+        elif form == 'no_alloc':
+            _check(lib.vectra_scan_top_k_no_alloc(ctypes.byref(args), stream))
         else:
             need = int(lib.vectra_scan_top_k_workspace_bytes(ctypes.byref(args)))
             if workspace is None:

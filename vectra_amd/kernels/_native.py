@@ -83,6 +83,8 @@ def scan_library() -> ctypes.CDLL:
         fn.restype = ctypes.c_int
     lib.vectra_scan_top_k_ws.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     lib.vectra_scan_top_k_ws.restype = ctypes.c_int
+    lib.vectra_scan_top_k_no_alloc.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.vectra_scan_top_k_no_alloc.restype = ctypes.c_int
     lib.vectra_scan_top_k_workspace_bytes.argtypes = [ctypes.c_void_p]
     lib.vectra_scan_top_k_workspace_bytes.restype = ctypes.c_int64
     lib.vectra_scan_status_string.argtypes = [ctypes.c_int]
