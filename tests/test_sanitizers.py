@@ -1,11 +1,12 @@
-"""The host code of both native libraries under AddressSanitizer and
+"""The host code of the native libraries under AddressSanitizer and
 UndefinedBehaviorSanitizer (CPU).
 
-`make -C vectra_amd/csrc sanitize-test` builds libvectra_rbf.so and
-libvectra_torch.so with their host code instrumented (argument validation,
-kernel selection, the operator's checks and its CPU implementation; device
-code as usual) into build/sanitize/lib, then runs tests/test_capi.py and
-tests/test_custom_op.py against them with clang's ASan runtime preloaded.
+`make -C vectra_amd/csrc sanitize-test` builds libvectra_rbf.so,
+libvectra_torch.so and libvectra_scan.so with their host code instrumented
+(argument validation, kernel selection, the split top-k's workspace sizing,
+the operator's checks and its CPU implementation; device code as usual) into
+build/sanitize/lib, then runs tests/test_capi.py, tests/test_custom_op.py and
+tests/test_scan_capi.py against them with clang's ASan runtime preloaded.
 Any sanitizer report aborts that run, so this test fails on it.
 """
 
