@@ -447,6 +447,35 @@ __device__ __forceinline__ float key_distance(uint64_t key) {
   return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
 }
 
+// Wave-wide operations on one 64-bit key per lane (lane shuffles: no LDS
+// buffer and no barrier).
+constexpr int kWaveLanes = 64;
+
+// Bitonic sort across the wave: lane i ends with the i-th smallest key.
+__device__ __forceinline__ uint64_t wave_sort(uint64_t key, int lane) {
+#pragma unroll
+  for (int size = 2; size <= kWaveLanes; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint64_t other = __shfl_xor(key, stride, kWaveLanes);
+      const bool keep_min = ((lane & stride) == 0) == ((lane & size) == 0);
+      const uint64_t lo = key < other ? key : other, hi = key < other ? other : key;
+      key = keep_min ? lo : hi;
+    }
+  }
+  return key;
+}
+
+// The smallest key of the wave, in every lane.
+__device__ __forceinline__ uint64_t wave_min(uint64_t key) {
+#pragma unroll
+  for (int mask = kWaveLanes / 2; mask > 0; mask >>= 1) {
+    const uint64_t other = __shfl_xor(key, mask, kWaveLanes);
+    key = other < key ? other : key;
+  }
+  return key;
+}
+
 // kTopKThreads threads; a 16-lane group loads kTopKCands candidates at once,
 // kSteps times per round of candidates between merge checks.
 template <bool kIds, int kTopKThreads, int kTopKCands, int kSteps>
@@ -494,6 +523,29 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
         __syncthreads();
       }
     }
+  };
+
+  // The first selection of a workgroup whose rounds hold at most a wave's
+  // worth of candidates: keys[0 .. k) are still empty and the n <= 64
+  // candidates sit at keys[k ..]; one wave sorts them in its lanes (a
+  // bitonic network over lane shuffles, where the LDS sort takes a barrier
+  // per stage), and the sorted keys, empty slots included, fill keys[0 ..).
+  auto first_select = [&](int n) {
+    if (tid < kWaveLanes) {
+      uint64_t key = tid < n ? keys[k + tid] : kNoKey;
+      key = wave_sort(key, tid);
+      if (tid < k) keys[tid] = key;
+    }
+    __syncthreads();
+  };
+  auto select = [&](bool first, int n) {
+    if constexpr (kTopKRound <= kWaveLanes) {
+      if (first && n <= kWaveLanes) {
+        first_select(n);
+        return;
+      }
+    }
+    merge(n);
   };
 
   uint64_t worst = kNoKey;  // the k-th best key so far; empty while fewer than k
@@ -562,14 +614,14 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
     // Merge once k candidates are in hand (the threshold then discards most
     // of the rest), and whenever the next round might not fit.
     if ((worst == kNoKey && n >= k) || n > kTopKKeys - k - kTopKRound) {
-      merge(n);
+      select(worst == kNoKey, n);
       if (tid == 0) fill = 0;
       worst = keys[k - 1];
       __syncthreads();
     }
   }
   const int n = static_cast<int>(fill);
-  if (n > 0) merge(n);
+  if (n > 0) select(worst == kNoKey, n);
   if (p.splits > 1) {
     // This range's k best to device memory, visible device-wide before the
     // arrival is counted: the barrier completes every wave's stores to this
@@ -588,7 +640,30 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
     const int all = p.splits * k;
     const uint64_t* parts = p.partial + q * p.splits * k;
     for (int i = tid; i < all; i += kTopKThreads) keys[i] = parts[i];
-    merge(all - k);
+    if (k <= kWaveLanes && p.splits <= kWaveLanes) {
+      // The ranges' lists are sorted: one wave merges them, lane i holding
+      // the head of range i; k times the smallest head is taken (the lowest
+      // lane on a tie) and its range advances.
+      __syncthreads();
+      if (tid < kWaveLanes) {
+        int pos = 0;
+        uint64_t head = tid < p.splits ? keys[tid * k] : kNoKey;
+        uint64_t mine = kNoKey;
+        for (int r = 0; r < k; ++r) {
+          const uint64_t m = wave_min(head);
+          const int win = __ffsll(static_cast<unsigned long long>(__ballot(head == m))) - 1;
+          if (tid == r) mine = m;
+          if (tid == win) {
+            ++pos;
+            head = pos < k ? keys[tid * k + pos] : kNoKey;
+          }
+        }
+        if (tid < k) keys[tid] = mine;
+      }
+      __syncthreads();
+    } else {
+      merge(all - k);
+    }
     if (tid == 0) p.arrived[q] = 0u;
   }
   for (int r = tid; r < k; r += kTopKThreads) {
