@@ -655,7 +655,7 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
           if (tid == r) mine = m;
           if (tid == win) {
             ++pos;
-            head = pos < k ? keys[tid * k + pos] : kNoKey;
+            head = tid < p.splits && pos < k ? keys[tid * k + pos] : kNoKey;
           }
         }
         if (tid < k) keys[tid] = mine;
