@@ -303,6 +303,22 @@ def test_nearest_over_a_large_shard():
     _check_nearest(q, rows, 10, msg='200k rows')
 
 
+@pytest.mark.parametrize('valid', [0, 7, 90])
+def test_split_ranges_with_few_or_no_valid_candidates(valid):
+    """Ranges whose candidates are mostly (or all) ids past the row count:
+    their lists end in empty slots, and the merge must still return exactly
+    the valid candidates, then +inf and NO_NODE."""
+    rng = np.random.default_rng(50 + valid)
+    rows = rng.standard_normal((100, 24)).astype(np.float32)
+    q = rng.standard_normal((2, 24)).astype(np.float32)
+    ids = rng.integers(100, 1000, 300).astype(np.uint32)  # past the rows: skipped
+    ids[rng.choice(300, valid, replace=False)] = rng.integers(0, 100, valid)
+    for k in (10, 64, 100):
+        print(f'split with {valid} valid candidates, k={k}', flush=True)
+        assert scan.workspace_bytes(_gpu(q), _gpu(rows), k, _gpu(ids)) > 0
+        _check_nearest(q, rows, k, ids, msg=f'valid={valid} k={k}')
+
+
 def test_split_workspace_is_reused_across_calls():
     """One workspace over calls of different sizes: each call leaves its
     arrival counters at zero, so the next one's merges start clean."""
