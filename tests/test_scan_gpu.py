@@ -319,6 +319,24 @@ def test_split_ranges_with_few_or_no_valid_candidates(valid):
         _check_nearest(q, rows, k, ids, msg=f'valid={valid} k={k}')
 
 
+@pytest.mark.parametrize('k,length,skipped', [(1000, 1030, 30), (993, 1031, 32), (1024, 1060, 20)])
+def test_split_range_merged_on_overflow_below_k(k, length, skipped):
+    """A range whose buffer overflows while it holds fewer than k keys (ids
+    past the row count skipped among its first 1024 candidates), then a short
+    last round: the range's earlier keys must survive the last selection
+    (tests/topk_model.py names the case).  Two ranges of `length` ids; every
+    form, no_alloc included, against the oracle."""
+    rng = np.random.default_rng(k + skipped)
+    n_rows, dim = 3000, 32
+    rows = rng.standard_normal((n_rows, dim)).astype(np.float32)
+    q = rng.standard_normal((1, dim)).astype(np.float32)
+    ids = rng.integers(0, n_rows, 2 * length).astype(np.uint32)
+    ids[rng.choice(1024, size=skipped, replace=False)] = n_rows + rng.integers(0, 500, skipped)
+    assert scan.workspace_bytes(_gpu(q), _gpu(rows), k, _gpu(ids)) > 0  # the split form is taken
+    print(f'split overflow below k: k={k} ids={2 * length} skipped={skipped}', flush=True)
+    _check_nearest(q, rows, k, ids, msg=f'overflow k={k}')
+
+
 def test_split_workspace_is_reused_across_calls():
     """One workspace over calls of different sizes: each call leaves its
     arrival counters at zero, so the next one's merges start clean."""

@@ -43,3 +43,27 @@ def test_no_alloc_top_k_equals_the_workspace_form_twice(ids):
         o_d, o_n = oracle.nearest(q, rows[:n], k, cand)
         np.testing.assert_array_equal(got_n.cpu().numpy(), o_n)
         np.testing.assert_array_equal(_bits(got_d), np.ascontiguousarray(o_d).view(np.int32))
+
+
+def test_no_alloc_top_k_with_ranges_merged_below_k():
+    """Large k over two ranges whose first 1024 ids hold some past the row
+    count: range 0's buffer overflows with fewer than k keys, then takes a
+    short last round.  Two calls in a row, the second smaller."""
+    rng = np.random.default_rng(41)
+    n_rows, dim = 3000, 32
+    rows = rng.standard_normal((n_rows, dim)).astype(np.float32)
+    for k, length, skipped in ((1024, 1060, 20), (1000, 1030, 30)):
+        q = rng.standard_normal((1, dim)).astype(np.float32)
+        ids = rng.integers(0, n_rows, 2 * length).astype(np.uint32)
+        ids[rng.choice(1024, size=skipped, replace=False)] = n_rows + 7
+        print(f'no-alloc top-k below k: k={k} ids={2 * length} skipped={skipped}', flush=True)
+        args = (_gpu(q), _gpu(rows), k, _gpu(ids))
+        assert scan.workspace_bytes(*args) > 0
+        want_d, want_n = scan.nearest(*args, form='split')
+        got_d, got_n = scan.nearest(*args, form='no_alloc')
+        torch.cuda.synchronize()
+        assert torch.equal(got_n, want_n)
+        np.testing.assert_array_equal(_bits(got_d), _bits(want_d))
+        o_d, o_n = oracle.nearest(q, rows, k, ids)
+        np.testing.assert_array_equal(got_n.cpu().numpy(), o_n)
+        np.testing.assert_array_equal(_bits(got_d), np.ascontiguousarray(o_d).view(np.int32))

@@ -526,7 +526,8 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
   };
 
   // The first selection of a workgroup whose rounds hold at most a wave's
-  // worth of candidates: keys[0 .. k) are still empty and the n <= 64
+  // worth of candidates: nothing has been selected yet, so keys[0 .. k) are
+  // still empty (not merely short of k keys), and the n <= 64
   // candidates sit at keys[k ..]; one wave sorts them in its lanes (a
   // bitonic network over lane shuffles, where the LDS sort takes a barrier
   // per stage), and the sorted keys, empty slots included, fill keys[0 ..).
@@ -549,6 +550,10 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
   };
 
   uint64_t worst = kNoKey;  // the k-th best key so far; empty while fewer than k
+  // Whether keys[0 .. k) hold a selection.  An overflow merge can keep fewer
+  // than k keys (ids past the rows are skipped), which leaves `worst` empty
+  // with keys in the buffer, so `worst` cannot tell an empty buffer.
+  bool selected = false;
   for (int64_t base = cand_begin; base < cand_end; base += kTopKRound) {
     // A round: kSteps steps of kTopKCands candidates per 16-lane group, a
     // step's loads issued before any of its sums (each candidate's own
@@ -614,14 +619,15 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
     // Merge once k candidates are in hand (the threshold then discards most
     // of the rest), and whenever the next round might not fit.
     if ((worst == kNoKey && n >= k) || n > kTopKKeys - k - kTopKRound) {
-      select(worst == kNoKey, n);
+      select(!selected, n);
+      selected = true;
       if (tid == 0) fill = 0;
       worst = keys[k - 1];
       __syncthreads();
     }
   }
   const int n = static_cast<int>(fill);
-  if (n > 0) select(worst == kNoKey, n);
+  if (n > 0) select(!selected, n);
   if (p.splits > 1) {
     // This range's k best to device memory, visible device-wide before the
     // arrival is counted: the barrier completes every wave's stores to this
