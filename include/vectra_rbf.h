@@ -119,12 +119,16 @@ typedef struct vectra_rbf_args {
  * VECTRA_FLAG_SPLIT_WEIGHTS: the tile kernel keeps every weight as a 16-bit
  * hi + lo pair (2^-17 of it).  By default, on key axes of 1024 keys or more
  * with no bias and scale >= 0, it first rounds each weight once to fp16 (2^-11
- * of it, one product instead of two) and keeps that result where every
- * query's weight sum is at least 256: its error is at most 2^-11 of the
- * spread of the values (the bound the reference accepts for fp16,
- * kernels/tests/test_parity.py:16-23), and in practice ~2^-11 / sqrt(sum) of
- * it.  Other kernels ignore the flag.  (No counterpart in the reference: its
- * kernel rounds the weights to the input dtype, spatial_rbf_attention.py:163.)
+ * of it, one product instead of two).  The rounding errors of independent
+ * weights add up like a random walk; the kernel bounds the walk's deviation
+ * per output from the weights' sums (sum w, sum w^2) and the largest |v|, and
+ * keeps the fp16 result for a work item only if four such deviations fit
+ * rtol 1e-3 / atol 1e-4 at every output and every weight sum is at least 256;
+ * otherwise (large values, weights held by few keys) the item runs the split.
+ * A pass whose bound misses twice over after an eighth of the keys stops
+ * there.  Other kernels ignore the flag.  (No counterpart in the reference:
+ * its kernel rounds the weights to the input dtype,
+ * spatial_rbf_attention.py:163.)
  */
 enum { VECTRA_FLAG_SPLIT_WEIGHTS = 1 };
 

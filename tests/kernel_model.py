@@ -27,8 +27,18 @@ a bias is present, gamma < 0, or any sum falls below the range.
 The tile kernel's fast pass (no bias, gamma >= 0, at least FAST_KEYS keys)
 comes first: each weight rounded once to fp16 (to nearest), no split, and the
 values in fp16 (bf16 values converted to nearest, 2^16 and beyond to inf).
-It stands if every sum of the work item is at least FAST_SUM and every
-accumulator is finite; otherwise the item takes the split pass above.
+It stands if every sum T of the work item is at least FAST_SUM, every output
+is finite, and at every output FAST_SIGMAS deviations of its rounding walk
+fit the 16-bit accuracy contract:
+
+  (FAST_WALK sqrt(sum_j w^_j^2) + 2^-25 Nk) / T * (max|v| + |o^|) + 2^-25
+      <= GATE_ATOL + GATE_RTOL |o^|
+
+(FAST_WALK = FAST_SIGMAS 2^-11 / sqrt(3); max|v| over the plane's values).
+After the first eighth of the key tiles the pass checks its course with the
+sums so far (the walk's term scaled to all keys, twice the allowance) and is
+abandoned early where even that fails.  Otherwise the item takes the split
+pass above.
 
 Each query's path is reported as SPLIT (one unshifted split pass), SHIFTED
 (recomputed with its maximum subtracted) or FAST.
@@ -49,6 +59,10 @@ SUM_RANGE = {'bf16': (F32(2.0 ** -32), F32(2.0 ** 32)), 'fp16': (F32(2.0 ** -3),
 TILE_ITEM_ROWS = 128  # query rows of one tile-kernel work item (4 waves x 2 blocks x 16)
 FAST_KEYS = 1024      # the tile kernel tries its fast pass from this many keys
 FAST_SUM = F32(256)   # and keeps it if every weight sum of the item is at least this
+FAST_SIGMAS = 4.0     # and this many deviations of its rounding walk fit the contract
+GATE_ATOL, GATE_RTOL = 1e-4, 1e-3  # the 16-bit paths' accuracy contract
+FAST_WALK = FAST_SIGMAS * 2.0 ** -11 / np.sqrt(3.0)
+TILE_KEYS = {32: 64, 64: 64, 128: 32}  # keys per tile, by head dim
 SPLIT, SHIFTED, FAST = 0, 1, 2  # per-query paths
 
 
@@ -92,12 +106,43 @@ def exp2_32(x):
 
 
 def _weighted_fast(x, v16):
-    """(acc, total) of the fast pass: fp16 weights (nearest) against fp16 values."""
+    """(acc, total, sum of squared weights) of the fast pass: fp16 weights
+    (nearest) against fp16 values."""
     w = exp2_32(x).astype(np.float16).astype(np.float64)
     with np.errstate(invalid='ignore', over='ignore'):
         acc = (w @ v16.astype(np.float64)).astype(F32)
         total = w.sum(-1).astype(F32)
-    return acc, total
+        wsq = (w * w).sum(-1).astype(F32)
+    return acc, total, wsq
+
+
+def fast_misses(acc, total, wsq, vmax, seen, n_k, slack=1.0):
+    """The tile kernel's check of its fast pass (rbf_tile_impl.h
+    fast_misses): per query, whether the bound misses the contract at an
+    output, a sum (scaled to n_k keys) is below FAST_SUM / slack, or an
+    output is not finite.  `seen` keys of n_k have been summed."""
+    grow = n_k / seen
+    t = total.astype(np.float64)
+    with np.errstate(invalid='ignore', over='ignore', divide='ignore'):
+        o = np.abs(acc.astype(np.float64) / t[:, None])
+        per_spread = (FAST_WALK * np.sqrt(wsq.astype(np.float64) / grow) + 2.0 ** -25 * seen) / t
+        est = per_spread[:, None] * (vmax + o) + 2.0 ** -25
+        ok = (est <= slack * (GATE_ATOL + GATE_RTOL * o)) & np.isfinite(o)
+    return ~(ok.all(-1) & (t * grow * slack >= FAST_SUM))
+
+
+def fast_pass(x0, v16, n_k, tile_keys=64):
+    """The fast pass over one work item: (acc, total, kept).  It checks its
+    course after the first eighth of the tiles (twice the allowance) and
+    keeps its result only if its final sums pass."""
+    tiles = -(-n_k // tile_keys)
+    seen = min(tiles // 8 * tile_keys, n_k)
+    acc, total, wsq = _weighted_fast(x0[:, :seen], v16[:seen])
+    if fast_misses(acc, total, wsq, np.abs(v16[:seen]).max(), seen, n_k, slack=2.0).any():
+        return None, None, False
+    acc, total, wsq = _weighted_fast(x0, v16)
+    kept = not fast_misses(acc, total, wsq, np.abs(v16).max(), n_k, n_k).any()
+    return acc, total, kept
 
 
 def _weighted(x, shift, v, kind, sum_of_weights=False):
@@ -182,8 +227,8 @@ def tile(q, k, v, gamma, bias, kind, one_pass=False, split_weights=False):
         rows = slice(r0, min(r0 + TILE_ITEM_ROWS, nq))
         x0 = fma32(coef, s[rows], c[None, :])
         if fast:
-            acc, total = _weighted_fast(x0, v16)
-            if np.isfinite(acc).all() and (total >= FAST_SUM).all():
+            acc, total, kept = fast_pass(x0, v16, k.shape[0], TILE_KEYS.get(q.shape[1], 64))
+            if kept:
                 out[rows] = _finish(acc, total)
                 path[rows] = FAST
                 continue

@@ -9,7 +9,8 @@ times below what a dropped lo part (2^-9 of every weight), a missed
 recompute (0 / 0 or overflow) or a wrong folded key value would change.  The
 cases are the 16-bit edge cases, which drive both kernels through both
 branches, and, against fp64, the large-norm cases where dropping the clamp matters
-most.
+most; and the tile kernel's long-key paths, config 4's values scaled by 1, 16
+and 256 among them.
 """
 
 import zlib
@@ -21,7 +22,7 @@ import torch
 from oracle import rbf as oracle
 from tests import kernel_model as km
 from tests.half_cases import HALF_CASES, HALF_KERNEL_SHAPES, half_case
-from tests.test_kernel_model import _concentrated, _large_norm_case, _long_keys
+from tests.test_kernel_model import _concentrated, _config4_plane, _large_norm_case, _long_keys
 from vectra_amd.kernels import capi
 
 pytestmark = pytest.mark.gpu
@@ -84,8 +85,14 @@ def _long_key_cases(kind):
     yield 'second_item_below_the_guard', (far, k, v, scale, bias), False, 128
     yield 'large_gamma', (q, k, v, torch.tensor(0.3), bias), False, 0
     yield 'few_live_keys', _concentrated(16, 16, kind), False, 0
-    yield 'guard_edge', _concentrated(0, 380, kind), False, 32
+    yield 'bound_edge', _concentrated(0, 380, kind), False, 0
     yield 'split_flag', (q, k, v, scale, bias), True, 0
+    # Values 16 times larger: abandoned at the course check.
+    yield 'values_x16', (q, k, (v * 16).to(KINDS[kind]).float(), scale, bias), False, 0
+    # Large values past the course check only: the final check sends it on.
+    late = v.clone()
+    late[..., 640:, :] *= 64
+    yield 'late_large_values', (q, k, late.to(KINDS[kind]).float(), scale, bias), False, 0
     if kind == 'bf16':
         big = v.clone()
         big[..., 7, 3] = 2.0 ** 17
@@ -101,3 +108,21 @@ def test_the_tile_kernel_follows_the_model_on_long_keys(kind):
         assert fast[:n_fast].all() and not fast[n_fast:].any(), name
         got = _kernel(q, k, v, scale, bias, KINDS[kind], 'tile', split_weights=split)
         np.testing.assert_allclose(got, want, err_msg=name, **MODEL_TOL)
+
+
+@pytest.mark.parametrize('kind', sorted(KINDS))
+def test_the_default_long_key_path_holds_the_gate_at_any_value_scale(kind):
+    """Config 4's q, k and gamma range on one plane of its 4096 keys, with
+    the values scaled by 1, 16 and 256: the default path (the fast pass where
+    its bound allows, the split otherwise) stays inside the 1e-3 / 1e-4 gate
+    against fp64, and follows the model's choice of path."""
+    for v_scale in (1.0, 16.0, 256.0):
+        for gamma in (0.005, 0.05):
+            q, k, v, scale, bias = _config4_plane(7 + int(v_scale), kind, gamma, v_scale)
+            print(f'config-4 plane: kind={kind} gamma={gamma} values x{v_scale:g}', flush=True)
+            want, path = km.run('tile', q, k, v, scale, bias, kind)
+            assert (path == (km.FAST if v_scale == 1.0 else km.SPLIT)).all()
+            got = _kernel(q, k, v, scale, bias, KINDS[kind], 'tile')
+            np.testing.assert_allclose(got, want, **MODEL_TOL)
+            exact = oracle.expanded_fp64(q, k, v, scale, bias)
+            np.testing.assert_allclose(got, exact, rtol=1e-3, atol=1e-4)

@@ -37,15 +37,26 @@
 // single pass first runs with each weight rounded once to fp16 (to nearest,
 // 2^-11 of the weight) and fp16 values (bf16 values converted to nearest as
 // they are staged: exact in fp16's normal range, within 2^-25 below it), one
-// product instead of the hi and lo pair and no split.  Its error is at most
-// 2^-11 of the spread of the values, the bound the reference accepts for
-// fp16 (kernels/tests/test_parity.py:16-23); rounding errors of independent
-// weights add up like a random walk, and a weight sum T >= kFastSum (each
-// weight is at most 1, so at least T keys carry the sum) keeps that walk
-// below 2^-11 / sqrt(T) of the spread.  If any query of the item ends with
-// T < kFastSum or a non-finite accumulator (a bf16 value of 2^16 or more
-// becomes inf in fp16, and inf times any weight, 0 included, is not finite),
-// the item takes the split pass as above.
+// product instead of the hi and lo pair and no split.  The result is the
+// exact weighted mean under the rounded weights w^_j = w_j + r_j, so output
+// o^ differs from o by sum_j r_j (v_j - o) / T (T = sum_j w^_j): the
+// rounding errors of independent weights add up like a random walk.  With
+// |r_j| <= 2^-11 w_j (normal fp16 weights; an error uniform over that step
+// has deviation 2^-11 w_j / sqrt(3)) and |v_j - o| <= max|v| + |o^|, the
+// walk's deviation is at most
+//     sigma = 2^-11 / sqrt(3) (max|v| + |o^|) sqrt(sum_j w^_j^2) / T,
+// plus 2^-25 per key (weights below fp16's normal range, worst case) and
+// 2^-25 for the values' conversion.  The item keeps the fast result only if
+// kFastSigmas * sigma + those terms fit the 16-bit paths' accuracy contract
+// (kGateAtol + kGateRtol |o^|) for every output, every weight sum T is at
+// least kFastSum (weights are at most 1, so at least T keys carry the sum
+// and the walk has that many terms), and every accumulator is finite (a bf16
+// value of 2^16 or more becomes inf in fp16, and inf times any weight, 0
+// included, is not finite); otherwise the item takes the split pass above.
+// sum_j w^_j^2 is the diagonal of the fp16 weights' product with
+// themselves (one more product per query block and key pair, the weight
+// fragment as both operands), and max|v| is taken over the values as they
+// are staged.
 //
 // Scheduling: persistent workgroups take items in a fixed order.  With a
 // grid and an item count that are multiples of the 8 XCDs (workgroups are
@@ -111,9 +122,15 @@ struct PassKind {
 };
 
 // The fast pass: tried for key axes of at least kFastKeys keys, kept if every
-// query's weight sum is at least kFastSum (see the header comment).
+// query's weight sum is at least kFastSum and kFastSigmas deviations of its
+// rounding error fit the accuracy contract of the 16-bit paths (rtol 1e-3,
+// atol 1e-4 against the eager fp32 result) at every output (see the header
+// comment).
 constexpr int32_t kFastKeys = 1024;
 constexpr float kFastSum = 256.f;
+constexpr float kFastSigmas = 4.f;
+constexpr float kGateAtol = 1e-4f, kGateRtol = 1e-3f;
+constexpr float kFastWalk = kFastSigmas * 0x1p-11f * 0.57735026919f;  // kFastSigmas 2^-11 / sqrt(3)
 
 // Three waves per SIMD (at most 168 VGPRs) measured fastest for head dims
 // up to 64; 128-dim heads keep two.
@@ -135,10 +152,17 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
   // below 2^-21 of a sum of at least 2^-3.
   constexpr bool kBf16 = __is_same(T, __bf16);
   constexpr float kSumLo = kBf16 ? 0x1p-32f : 0x1p-3f;
+  typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+  // Fast pass statistic: the largest |v| this thread staged in the pass (fp32
+  // for bf16 inputs, packed fp16 for fp16 inputs).
+  float vmax = 0.f;
+  h2v vmax16 = {0, 0};
 
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ int32_t exact_flag[2];
   __shared__ int32_t split_flag[2];  // the fast pass did not hold
+  __shared__ float vmax_wave[2][kWaves];  // the fast pass's max |v| per wave
+  __shared__ int32_t abort_flag[2];  // the fast pass was abandoned early
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -215,7 +239,8 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
   // c_j = log2(e) bias_j - coef |k_j|^2 / 2 (-inf past Nk).  A fast pass
   // stores bf16 values as fp16 (to nearest).
   auto publish = [&](const Stage& st, int32_t tile, int buf, float coef, auto kind_c) {
-    constexpr bool kToF16 = decltype(kind_c)::value == kPassFast && kBf16;
+    constexpr bool kFast = decltype(kind_c)::value == kPassFast;
+    constexpr bool kToF16 = kFast && kBf16;
     const int32_t j0 = tile * kKeys;
     T* kl = reinterpret_cast<T*>(lds + buf * G::kBufBytes);
     T* vl = reinterpret_cast<T*>(lds + buf * G::kBufBytes + G::kKBytes);
@@ -236,8 +261,17 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float f0 = __uint_as_float(w[e] << 16), f1 = __uint_as_float(w[e] & 0xffff0000u);
+            // IEEE maximum (v_maximum3_f32): no quieting copies of the inputs.
+            vmax = __builtin_elementwise_maximum(
+                vmax, __builtin_elementwise_maximum(__builtin_fabsf(f0), __builtin_fabsf(f1)));
             w[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{f0, f1}, h2));
           }
+        } else if constexpr (kFast) {
+          // fp16 values: |v| by clearing the sign bits, a packed maximum.
+          const uint32_t* w = reinterpret_cast<const uint32_t*>(&vw);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            vmax16 = __builtin_elementwise_maximum(vmax16, __builtin_bit_cast(h2v, w[e] & 0x7fff7fffu));
         }
         if (j0 + kKeys > n_k && j0 + key >= n_k) vw = make_uint4(0, 0, 0, 0);  // the last tile only
         *reinterpret_cast<uint4*>(vl + key * G::kVStride + d0) = vw;
@@ -266,6 +300,9 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
   float row_max[kCB];
   f32x4 acc[kCB][kDTiles];
   f32x4 total[kCB];
+  // Fast pass statistic: each query block's fp16 weights times themselves;
+  // the diagonal holds every query's sum of squared weights.
+  f32x4 wsq[kCB];
 
   // Reduces tile `buf` for the wave's 32 queries.
   auto compute = [&](int buf, float coef, auto kind_c) {
@@ -323,6 +360,7 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
             wp[2 * hb] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{w[0], w[1]}, h2));
             wp[2 * hb + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{w[2], w[3]}, h2));
           }
+
           pw[cb] = __builtin_bit_cast(typename H::Qk, make_uint4(wp[0], wp[1], wp[2], wp[3]));
         }
 #pragma unroll
@@ -338,7 +376,10 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
         const uint32_t one_h = MfmaOps<_Float16>::kOnePair;
         const auto ones_h = __builtin_bit_cast(typename H::Qk, make_uint4(one_h, one_h, one_h, one_h));
 #pragma unroll
-        for (int cb = 0; cb < kCB; ++cb) total[cb] = H::qk(ones_h, pw[cb], total[cb]);
+        for (int cb = 0; cb < kCB; ++cb) {
+          total[cb] = H::qk(ones_h, pw[cb], total[cb]);
+          wsq[cb] = H::qk(pw[cb], pw[cb], wsq[cb]);  // A = B^T (the same lane layout)
+        }
         __builtin_amdgcn_sched_barrier(0);
         continue;
       }
@@ -387,10 +428,50 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
     }
   };
 
+  // Whether, with the fast pass's sums so far over `seen` keys, the bound on
+  // its error misses the accuracy contract at one of this lane's outputs:
+  // kFastSigmas deviations of the walk (its bound per unit of spread scaled
+  // from `seen` keys to all n_k, as sqrt(sum w^2) / T falls like one over
+  // the root of the key count), 2^-25 per key and for the values, against
+  // `slack` times the allowance; also a weight sum (scaled to n_k keys) below
+  // kFastSum / slack, or a non-finite output.
+  auto fast_misses = [&](float v_max, float seen, float slack) {
+    const float grow = static_cast<float>(n_k) / seen;
+    bool miss = false;
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb) {
+      const float t = total[cb][0];
+      miss = miss || !(t * grow * slack >= kFastSum);
+      // Sum of squared weights of this lane's query: row `col` of the
+      // product, held by lane col + 16 (col / 4) in register col % 4.
+      const float diag = wsq[cb][col & 3];
+      const float sq_w = __shfl(diag, col + 16 * (col >> 2), kWave);
+      const float inv_t = 1.f / t;
+      const float per_spread = (kFastWalk * __builtin_sqrtf(sq_w / grow) + 0x1p-25f * seen) * inv_t;
+#pragma unroll
+      for (int u = 0; u < kDTiles; ++u) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float o = __builtin_fabsf(acc[cb][u][r] * inv_t);
+          miss = miss || !__builtin_isfinite(o) ||
+                 !(fmaf(per_spread, v_max + o, 0x1p-25f) <= slack * fmaf(kGateRtol, o, kGateAtol));
+        }
+      }
+    }
+    return miss;
+  };
+
   // One pass of an item over every key tile (double-buffered, one barrier
-  // per tile).  Every wave of the workgroup runs it.
+  // per tile).  Every wave of the workgroup runs it.  The fast pass checks
+  // its course after the first eighth of the tiles and is abandoned (returns
+  // false, nothing left in flight) where its bound, so far, misses the
+  // contract by more than twice: the split pass then runs instead.  That is
+  // a prediction, not the test: a fast pass that runs to the end is kept
+  // only if its final sums pass it.
   Stage st;
+  int32_t parity = 0;
   auto run_pass = [&](const Coords& c, float coef, auto kind_c) {
+    constexpr bool kFast = decltype(kind_c)::value == kPassFast;
     if constexpr (decltype(kind_c)::value != kPassMax) {
 #pragma unroll
       for (int cb = 0; cb < kCB; ++cb) {
@@ -399,24 +480,46 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
         total[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
+    if constexpr (decltype(kind_c)::value == kPassFast) {
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) wsq[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      vmax = 0.f;
+      vmax16 = h2v{0, 0};
+    }
     issue(st, c, 0);
     publish(st, 0, 0, coef, kind_c);
     __syncthreads();
     if (tiles > 1) issue(st, c, 1);
+    const int32_t probe = tiles / 8;  // tiles reduced when the fast pass checks its course
     for (int32_t t = 0; t < tiles; ++t) {
       compute(t & 1, coef, kind_c);
       if (t + 1 < tiles) publish(st, t + 1, (t + 1) & 1, coef, kind_c);
+      if constexpr (kFast) {
+        // After the staging registers are written out: no loads in flight.
+        if (t + 1 == probe) {
+          const float m = kBf16 ? vmax : fmaxf(static_cast<float>(vmax16.x), static_cast<float>(vmax16.y));
+          const float seen = static_cast<float>(min(probe * kKeys, n_k));
+          if (__builtin_amdgcn_ballot_w64(fast_misses(reduce_wave(m, OpMax()), seen, 2.f)) && lane == 0)
+            abort_flag[parity] = 1;
+        }
+      }
       __syncthreads();
+      if constexpr (kFast) {
+        // Every wave reads the flag after the barrier: a uniform exit, with
+        // tile t + 1 already staged and nothing issued past it.
+        if (t + 1 == probe && abort_flag[parity] != 0) return false;
+      }
       if (t + 2 < tiles) issue(st, c, t + 2);
     }
+    return true;
   };
 
-  int32_t parity = 0;
   for (int32_t slot = static_cast<int32_t>(blockIdx.x); slot < items; slot += grid, parity ^= 1) {
     const Coords c = coords(item_of(slot));
     if (tid == 0) {  // read after the first barrier of this item
       exact_flag[parity] = 0;
       split_flag[parity] = 0;
+      abort_flag[parity] = 0;
     }
     const float coef = 2.f * kLog2e * load_any(p.scale, c.b * p.ssb + c.h * p.ssh, p.scale_dtype);
     // Query rows of this wave: item rows (wave * kCB + cb) * 16 + col (rows
@@ -440,23 +543,23 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
     bool exact = has_bias || !(coef >= 0.f);
     bool split = true;
     if (!exact && n_k >= kFastKeys && !(p.flags & VECTRA_FLAG_SPLIT_WEIGHTS)) {
-      run_pass(c, coef, PassKind<kPassFast>{});
-      // A weight sum below kFastSum (or NaN), or a non-finite accumulator (a
-      // value fp16 cannot hold), anywhere in the workgroup sends the item to
-      // the split pass.  A finite accumulator is at most Nk * 2^16 < 2^47 in
-      // size, so their sum is finite exactly when every one of them is.
-      float acc_sum = 0.f;
-      bool redo = false;
+      // The fast result stands if the whole pass ran and its final sums pass
+      // the check anywhere in the workgroup: every weight sum at least
+      // kFastSum, every output finite and within the contract by its bound.
+      if (run_pass(c, coef, PassKind<kPassFast>{})) {
+        // The workgroup's max |v| (every wave staged a share of every tile).
+        const float m = kBf16 ? vmax : fmaxf(static_cast<float>(vmax16.x), static_cast<float>(vmax16.y));
+        const float mw = reduce_wave(m, OpMax());
+        if (lane == 0) vmax_wave[parity][wave] = mw;
+        __syncthreads();
+        float v_max = vmax_wave[parity][0];
 #pragma unroll
-      for (int cb = 0; cb < kCB; ++cb) {
-        redo = redo || !(total[cb][0] >= kFastSum);
-#pragma unroll
-        for (int u = 0; u < kDTiles; ++u) acc_sum += (acc[cb][u][0] + acc[cb][u][1]) + (acc[cb][u][2] + acc[cb][u][3]);
+        for (int w = 1; w < kWaves; ++w) v_max = fmaxf(v_max, vmax_wave[parity][w]);
+        const bool redo = fast_misses(v_max, static_cast<float>(n_k), 1.f);
+        if (__builtin_amdgcn_ballot_w64(redo) && lane == 0) split_flag[parity] = 1;
+        __syncthreads();
+        split = split_flag[parity] != 0;
       }
-      redo = redo || !__builtin_isfinite(acc_sum);
-      if (__builtin_amdgcn_ballot_w64(redo) && lane == 0) split_flag[parity] = 1;
-      __syncthreads();
-      split = split_flag[parity] != 0;
     }
     if (!exact && split) {
       run_pass(c, coef, PassKind<kPassSum>{});
