@@ -210,3 +210,40 @@ def test_two_stage_failures_stay_with_their_batch():
     assert isinstance(results[1][0], ValueError)
     assert isinstance(results[2][0], KeyError)
     assert results[3][0].value == 70
+
+
+def test_close_cancels_batches_in_flight_and_being_launched():
+    """close() while one batch is in flight (finish blocked) and the next is
+    being launched (launch blocked): every caller is released with
+    CancelledError instead of waiting forever, and later submissions are
+    refused."""
+    release = threading.Event()
+    launched = []
+
+    def launch(items):
+        launched.append(list(items))
+        if len(launched) > 1:
+            release.wait(5)
+        return list(items)
+
+    def finish(handle):
+        release.wait(5)
+        return [item + 1 for item in handle]
+
+    async def main():
+        b = batcher_lib.Batcher(max_batch_size=2, window_s=0.0, launch=launch, finish=finish, depth=2)
+        b.start()
+        calls = [asyncio.ensure_future(b.submit(i)) for i in range(6)]
+        while len(launched) < 2:
+            await asyncio.sleep(0.005)
+        closing = asyncio.ensure_future(b.close())
+        await asyncio.sleep(0.05)
+        release.set()  # let the blocked threads return, so shutdown completes
+        await asyncio.wait_for(closing, 5)
+        outcomes = await asyncio.wait_for(asyncio.gather(*calls, return_exceptions=True), 5)
+        with pytest.raises(RuntimeError, match='closed'):
+            await b.submit(9)
+        return outcomes
+
+    outcomes = asyncio.run(main())
+    assert all(isinstance(o, asyncio.CancelledError) for o in outcomes), outcomes

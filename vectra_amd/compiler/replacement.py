@@ -19,9 +19,7 @@ import torch
 from torch import fx
 
 from vectra_amd.compiler import pattern
-
-# Imported for its side effect: registering torch.ops.vectra.rbf_attention.
-from vectra_amd.kernels import custom_ops  # noqa: F401  # pylint: disable=unused-import
+from vectra_amd.kernels import custom_ops
 
 aten = torch.ops.aten
 SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
@@ -177,7 +175,7 @@ def make_replacement(spec: pattern.PatternSpec):
             )
         bias = inputs[pattern.BIAS] if spec.has_bias else None
         out = graph.call_function(
-            torch.ops.vectra.rbf_attention.default,
+            custom_ops.overload(),
             (inputs[pattern.Q], inputs[pattern.K], value, scale, bias),
         )
         graph.output(out)

@@ -37,6 +37,12 @@ def _rbf_attention_fake(q, k, v, scale, key_bias=None):
     return q.new_empty((*q.shape[:-1], v.shape[-1]), dtype=v.dtype)
 
 
+def overload() -> torch._ops.OpOverload:
+    """The operator's default overload, the node target a graph rewrite
+    emits (defined once this module has loaded the extension)."""
+    return torch.ops.vectra.rbf_attention.default
+
+
 def rbf_attention(q, k, v, scale, key_bias=None):
     """Python-level alias of torch.ops.vectra.rbf_attention."""
     return torch.ops.vectra.rbf_attention(q, k, v, scale, key_bias)

@@ -24,6 +24,12 @@ launches run in order on one thread and completions in the same order on
 another, so the next batch's host-to-device copy overlaps the model's work on
 the previous one.  A single `run_batch` function is the depth-1 form, in
 which batches never overlap.
+
+Every submitted request's future is tracked until it is done.  `close`
+stops batching and cancels every request not yet resolved: those still
+waiting, the batch being launched and the batches in flight (their callers
+see asyncio.CancelledError; work already queued on the device finishes,
+and its results are dropped).  Requests submitted after `close` are refused.
 """
 
 import asyncio
@@ -99,6 +105,10 @@ class Batcher(typing.Generic[_Item, _Result]):
         self._waiting: collections.deque[_Pending] = collections.deque()
         self._arrival: asyncio.Event | None = None
         self._task: asyncio.Task | None = None
+        self._closed = False
+        # Futures of every request submitted and not yet done: waiting,
+        # being launched or in flight.
+        self._unresolved: set[asyncio.Future] = set()
         self._launch_thread = concurrent.futures.ThreadPoolExecutor(max_workers=1, thread_name_prefix='inference')
         self._finish_thread = concurrent.futures.ThreadPoolExecutor(max_workers=1, thread_name_prefix='completion')
 
@@ -110,13 +120,15 @@ class Batcher(typing.Generic[_Item, _Result]):
         self._task = asyncio.get_running_loop().create_task(self._serve())
 
     async def close(self) -> None:
-        """Stops batching; requests still waiting are cancelled."""
+        """Stops batching; every request not yet resolved is cancelled."""
+        self._closed = True
         task, self._task = self._task, None
         if task is not None:
             task.cancel()
             await asyncio.gather(task, return_exceptions=True)
-        while self._waiting:
-            self._waiting.popleft().future.cancel()
+        self._waiting.clear()
+        for future in list(self._unresolved):
+            future.cancel()
         self._launch_thread.shutdown(wait=True)
         self._finish_thread.shutdown(wait=True)
 
@@ -127,7 +139,11 @@ class Batcher(typing.Generic[_Item, _Result]):
         """
         if self._arrival is None:
             raise RuntimeError('Batcher.start() was not called')
+        if self._closed:
+            raise RuntimeError('the Batcher is closed')
         future = asyncio.get_running_loop().create_future()
+        self._unresolved.add(future)
+        future.add_done_callback(self._unresolved.discard)
         self._waiting.append(_Pending(item, future, time.perf_counter()))
         self._arrival.set()
         return await future
