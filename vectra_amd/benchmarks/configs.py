@@ -6,6 +6,12 @@ the parity gates are quoted on.  Inputs are drawn on the CPU from
 counts, as fp32 ``randn`` then cast and moved, as the reference's parity
 tests draw theirs (kernels/tests/test_parity.py:49-61).  A valid count c_b
 masks keys j >= c_b of batch b with a -inf key bias.
+
+A configuration with `fused_qkv` draws one [B, N, 3 H D] tensor instead, and
+q, k and v are head-transposed views of its three thirds, [B, N, H, D] ->
+[B, H, N, D] (rows of D elements, 3 H D apart): the layout the price
+model's attention sites hand the operator, a slice of one qkv projection
+(models/price_transformer/spatial_attention.py:80-87 of the reference).
 """
 
 import dataclasses
@@ -32,6 +38,7 @@ class Config:
     valid: tuple[int, int] | None
     qk_std: float = 1.0
     bias_dtype: torch.dtype | None = None  # default: the input dtype
+    fused_qkv: bool = False  # q, k, v as head-transposed views of one projection
 
     @property
     def value_dim(self) -> int:
@@ -63,8 +70,13 @@ LONG_KEY = Config('long_key', 16, 16, 4096, 4096, 64, torch.bfloat16, (0.005, 0.
 # The reference's bandwidth-proof workload (kernels/benchmarks/bandwidth.py:44-57,
 # throughput.py:97-111): fp16, gamma = 1/(2D) in every head, the last 8 keys padded.
 BANDWIDTH = Config('bandwidth', 1024, 4, 65, 65, 32, torch.float16, (1.0 / 64, 1.0 / 64), (57, 57))
+# One attention site of the config-5 price model (d_model 128, 8 heads of 16
+# dims, 1024 subjects x (1 + 64 comparables)) with fp16 blocks: q, k, v as
+# views of the qkv projection; gamma = 1 / (2 sigma^2) at the model's initial
+# sigma^2 = 16 (the head width); the subject and 8-64 comparables valid.
+MODEL_SITE = Config('model_site', 1024, 8, 65, 65, 16, torch.float16, 1.0 / 32, (9, 65), fused_qkv=True)
 
-CONFIGS = {c.name: c for c in (CPU_EAGER, SERVING, SELF_ATTENTION, LONG_KEY, BANDWIDTH)}
+CONFIGS = {c.name: c for c in (CPU_EAGER, SERVING, SELF_ATTENTION, LONG_KEY, BANDWIDTH, MODEL_SITE)}
 
 
 @dataclasses.dataclass
@@ -83,7 +95,16 @@ class Inputs:
         def move(t):
             return None if t is None else t.to(device)
 
-        return Inputs(*(move(t) for t in dataclasses.astuple(self)))
+        base = self.q._base  # pylint: disable=protected-access
+        shared = base is not None and all(t._base is base for t in (self.k, self.v))  # pylint: disable=protected-access
+        if shared and base.is_contiguous():
+            # Views of one projection: move it once and view it the same way
+            # there (moving each view alone would make it contiguous).
+            moved = base.to(device)
+            q, k, v = (moved.as_strided(t.shape, t.stride(), t.storage_offset() - base.storage_offset())
+                       for t in (self.q, self.k, self.v))
+            return Inputs(q, k, v, move(self.scale), move(self.key_bias), move(self.counts))
+        return Inputs(*(move(getattr(self, f.name)) for f in dataclasses.fields(self)))
 
     def nbytes(self) -> int:
         return sum(
@@ -103,9 +124,15 @@ def make_inputs(config: Config, seed: int = 0, device='cpu', batch: int | None =
         x = torch.randn(*size, generator=gen)
         return (x * std if std != 1.0 else x).to(config.dtype)
 
-    q = randn(b, h, config.n_q, d, std=config.qk_std)
-    k = randn(b, h, config.n_k, d, std=config.qk_std)
-    v = randn(b, h, config.n_k, config.value_dim)
+    if config.fused_qkv:
+        if config.n_q != config.n_k or config.value_dim != d or config.qk_std != 1.0:
+            raise ValueError('a fused projection has one token axis, one head width and unit values')
+        qkv = randn(b, config.n_q, 3 * h * d)
+        q, k, v = (t.view(b, config.n_q, h, d).transpose(1, 2) for t in qkv.split(h * d, dim=-1))
+    else:
+        q = randn(b, h, config.n_q, d, std=config.qk_std)
+        k = randn(b, h, config.n_k, d, std=config.qk_std)
+        v = randn(b, h, config.n_k, config.value_dim)
     if isinstance(config.gamma, tuple):
         lo, hi = config.gamma
         scale = lo + (hi - lo) * torch.rand(1, h, 1, 1, generator=gen)
