@@ -9,6 +9,7 @@ rocprofv3's kernel-stats and counter-collection CSVs.
 import csv
 
 import pytest
+import torch
 
 from vectra_amd.benchmarks import bandwidth_proof
 from vectra_amd.benchmarks import configs
@@ -129,3 +130,13 @@ def test_bandwidth_workload_is_the_reference_harness_shape():
     # The harness's five rotating input sets do not fit the Infinity Cache.
     assert 5 * roofline.fused_bytes(c.shape()) > roofline.MI355X.infinity_cache_bytes
     assert 5 * roofline.fused_bytes(configs.SERVING.shape()) > roofline.MI355X.infinity_cache_bytes
+
+
+def test_read_write_stream_checks_its_byte_mix():
+    """The read + write ceiling's argument checks, before any launch."""
+    from vectra_amd.benchmarks import read_ceiling
+    sink = torch.zeros(256, dtype=torch.int32)
+    for read_bytes, write_bytes in ((160, 16), (16, 32), (64, 8), (40, 24)):
+        with pytest.raises(ValueError):
+            read_ceiling.read_write_once(torch.zeros(read_bytes, dtype=torch.uint8),
+                                         torch.zeros(write_bytes, dtype=torch.uint8), sink, 1, None)

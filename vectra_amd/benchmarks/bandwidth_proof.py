@@ -35,7 +35,10 @@ reads from its serving SLO:
 The analytic budgets of `vectra_amd.benchmarks.roofline` are reported
 beside the counters, and with `--read-ceiling` so is a plain read of the
 fused bytes measured the same way (`eager_gpu --impl read`): what the
-hardware itself reaches with one call at a time.  Exits 1 when a gate fails.
+hardware itself reaches with one call at a time; where the output is at
+least an eighth of the reads (the self-attention shapes), also a plain kernel
+streaming the same reads and writes (`eager_gpu --impl readwrite`), and the
+fused kernel's share of it.  Exits 1 when a gate fails.
 """
 
 import argparse
@@ -194,7 +197,14 @@ def main(argv=None) -> int:
         measured[batch] = {impl: measure(args.config, batch, impl, work, scales, args.reps)
                            for impl in ('eager', 'fused')}
         if args.read_ceiling:
-            ceilings[batch] = measure(args.config, batch, 'read', work, scales, args.reps)
+            ceilings[batch] = {'read': measure(args.config, batch, 'read', work, scales, args.reps)}
+            shape = dataclasses.replace(config, batch=batch).shape()
+            out_bytes = shape.planes * shape.n_q * shape.value_dim * shape.element_bytes
+            if out_bytes * 8 >= roofline.fused_bytes(shape) - out_bytes:
+                mixed = measure(args.config, batch, 'readwrite', work, scales, args.reps)
+                # The fused kernel's rate as a share of the plain stream's.
+                mixed['fused_share'] = mixed['kernel_ns'] / measured[batch]['fused']['kernel_ns']
+                ceilings[batch]['read_write'] = mixed
         budgets[batch] = roofline.analyze(dataclasses.replace(config, batch=batch).shape())
     failures = evaluate(measured)
     report = {'config': args.config, 'copy_scales': scales, 'measured': measured,

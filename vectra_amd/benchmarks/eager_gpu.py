@@ -10,7 +10,10 @@ is cast to the input dtype first, as the reference's benchmarks do
 (kernels/benchmarks/throughput.py:129-131), so the chain stays in that dtype.
 
 `--impl read` is a plain HBM read of the fused operator's algorithmic
-bytes instead: the ceiling the hardware reaches under the same timing.
+bytes instead: the ceiling the hardware reaches under the same timing;
+`--impl readwrite` streams the operator's reads in and its output's bytes
+out in one launch (at most 8 bytes read per byte written, so not the serving
+shape's 1 in 133): the ceiling of a kernel with the operator's mix.
 
 The script runs the chosen implementation `--reps` times over rotating input
 sets (after one warm-up call per set) and prints one JSON line with the
@@ -70,9 +73,30 @@ def read_region(config, batch, n_sets):
     return [lambda b=b: read_ceiling.read_once(b, sink, blocks, stream) for b in bufs]
 
 
+def read_write_region(config, batch, n_sets):
+    """One launch per call streaming the fused operator's reads in and its
+    output's bytes out, one pair of buffers per input set (built on the host
+    and copied, so the only kernel of a call is the stream)."""
+    from vectra_amd.benchmarks import read_ceiling  # pylint: disable=import-outside-toplevel
+    from vectra_amd.benchmarks import roofline  # pylint: disable=import-outside-toplevel
+    import dataclasses  # pylint: disable=import-outside-toplevel
+
+    shape = dataclasses.replace(config, batch=batch or config.batch).shape()
+    out_bytes = shape.planes * shape.n_q * shape.value_dim * shape.element_bytes
+    read_bytes = (roofline.fused_bytes(shape) - out_bytes + 15) // 16 * 16
+    write_bytes = (out_bytes + 15) // 16 * 16
+    gen = torch.Generator().manual_seed(0)
+    srcs = [torch.randint(0, 256, (read_bytes,), dtype=torch.uint8, generator=gen).to('cuda') for _ in range(n_sets)]
+    dsts = [torch.zeros(write_bytes, dtype=torch.uint8).to('cuda') for _ in range(n_sets)]
+    blocks = torch.cuda.get_device_properties(0).multi_processor_count * 8
+    sink = torch.zeros(blocks * read_ceiling.THREADS, dtype=torch.int32).to('cuda')
+    stream = torch.cuda.current_stream()
+    return [lambda s=s, d=d: read_ceiling.read_write_once(s, d, sink, blocks, stream) for s, d in zip(srcs, dsts)]
+
+
 def main():
     p = argparse.ArgumentParser()
-    p.add_argument('--impl', choices=sorted(IMPLS) + ['read'], required=True)
+    p.add_argument('--impl', choices=sorted(IMPLS) + ['read', 'readwrite'], required=True)
     p.add_argument('--config', default='serving', choices=sorted(configs.CONFIGS))
     p.add_argument('--sets', type=int, default=5)
     p.add_argument('--reps', type=int, default=20)
@@ -81,6 +105,8 @@ def main():
     config = configs.CONFIGS[args.config]
     if args.impl == 'read':
         calls_of_set = read_region(config, args.batch, args.sets)
+    elif args.impl == 'readwrite':
+        calls_of_set = read_write_region(config, args.batch, args.sets)
     else:
         fn = IMPLS[args.impl]
         sets = [configs.make_inputs(config, seed=s, batch=args.batch).to('cuda') for s in range(args.sets)]

@@ -53,6 +53,20 @@ def read_once(buf: torch.Tensor, sink: torch.Tensor, blocks: int, stream: torch.
         raise RuntimeError(f'vectra_bench_read_stream failed with status {status}')
 
 
+def read_write_once(src: torch.Tensor, dst: torch.Tensor, sink: torch.Tensor, blocks: int,
+                    stream: torch.cuda.Stream) -> None:
+    """One launch streaming all of `src` in and all of `dst` out."""
+    read_bytes, write_bytes = src.numel() * src.element_size(), dst.numel() * dst.element_size()
+    if sink.numel() < blocks * THREADS:
+        raise ValueError('sink holds fewer than blocks * 256 words')
+    if not 16 <= write_bytes <= read_bytes or read_bytes // write_bytes > 8 or (read_bytes | write_bytes) % 16:
+        raise ValueError('needs 16-byte multiples with 16 <= write_bytes <= read_bytes <= 8 * write_bytes')
+    status = _lib().vectra_bench_read_write_stream(src.data_ptr(), read_bytes, dst.data_ptr(), write_bytes,
+                                                   sink.data_ptr(), blocks, ctypes.c_void_p(stream.cuda_stream))
+    if status != 0:
+        raise RuntimeError(f'vectra_bench_read_write_stream failed with status {status}')
+
+
 def measure(nbytes: int, trials: int = 20, per_trial: int = 100, blocks: int | None = None) -> dict:
     """Median time of one read of `nbytes` from HBM, in a HIP graph."""
     nbytes = (nbytes + 15) // 16 * 16
@@ -109,10 +123,7 @@ def measure_read_write(read_bytes: int, write_bytes: int, trials: int = 20, per_
     sink = torch.zeros(blocks * THREADS, dtype=torch.int32, device='cuda')
 
     def launch(i, stream):
-        status = _lib().vectra_bench_read_write_stream(srcs[i].data_ptr(), read_bytes, dsts[i].data_ptr(), write_bytes,
-                                                       sink.data_ptr(), blocks, ctypes.c_void_p(stream.cuda_stream))
-        if status != 0:
-            raise RuntimeError(f'vectra_bench_read_write_stream failed with status {status}')
+        read_write_once(srcs[i], dsts[i], sink, blocks, stream)
 
     stream = torch.cuda.current_stream()
     for i in range(n_sets):
