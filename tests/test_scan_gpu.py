@@ -188,6 +188,35 @@ def test_adc_with_unaligned_codes_and_ids():
     _same(got, want, 'unaligned adc with ids')
 
 
+def test_adc_stream_over_several_grid_strides():
+    # The 16-byte ADC kernel (the engine's 16 sub-spaces) over more codes
+    # than one pass of its grid covers, ending mid-stride; a table whose rows
+    # start 4 bytes past a 16-byte boundary (staged word by word); ids past
+    # the codes; and ids into an empty code set (every distance NaN).
+    rng = np.random.default_rng(31)
+    m, n = 16, (1 << 20) + 12345
+    codes = rng.integers(0, 256, (n, m), dtype=np.uint8)
+    wide = (rng.standard_normal((2, m * 256 + 3)) * 7).astype(np.float32)
+    tables_np = np.ascontiguousarray(wide[:, 1:1 + m * 256])
+    tables = _gpu(wide)[:, 1:1 + m * 256]
+    assert tables.data_ptr() % 16 == 4
+    codes_gpu = _gpu(codes)
+    print(f'adc stream n {n}', flush=True)
+    got = scan.pq_adc_distances(tables, codes_gpu)
+    _same(got, np.stack([oracle.pq_adc(tables_np[i], codes) for i in range(2)]), 'adc stream')
+    ids_np = rng.integers(0, n + n // 50, 700_001).astype(np.int32)
+    got = scan.pq_adc_distances(tables, codes_gpu, ids=torch.from_numpy(ids_np).cuda())
+    want = np.full((2, ids_np.shape[0]), np.nan, np.float32)
+    ok = ids_np < n
+    assert 0 < (~ok).sum() < ok.sum()
+    for i in range(2):
+        want[i, ok] = oracle.pq_adc(tables_np[i], codes[ids_np[ok]])
+    _same(got, want, 'adc stream with ids')
+    empty = torch.zeros(0, m, dtype=torch.uint8, device='cuda')
+    got = scan.pq_adc_distances(tables, empty, ids=torch.arange(5, dtype=torch.int32, device='cuda'))
+    assert got.shape == (2, 5) and torch.isnan(got).all()
+
+
 @pytest.mark.parametrize('dim,m', [(128, 16), (128, 8), (96, 32), (256, 8), (48, 3), (512, 16), (17, 17), (272, 8)])
 def test_tables_against_the_oracle(dim, m):
     rng = np.random.default_rng(dim + m)

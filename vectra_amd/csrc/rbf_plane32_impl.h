@@ -78,7 +78,6 @@ __global__ __launch_bounds__(64 * ((kKeys / 16 + 1) / 2)) void rbf_plane32_kerne
   // when the workgroup has at least kPieces / 256 waves (three for 65 queries
   // over 80 keys of 32 dims); smaller workgroups loop for the rest.
   constexpr int kRounds = 4;
-  typedef float f32x4v __attribute__((ext_vector_type(4)));
 
   __shared__ __align__(16) float vt_lds[kD * G::kVtStride];
   __shared__ __align__(16) char k_lds[kKeys * G::kKStride];

@@ -197,7 +197,8 @@ struct PqAdc {
   int64_t table_stride, code_stride, out_stride;
   int64_t num_codes, num_cand;
   int32_t subspaces;
-  int32_t words;  // codes may be read as 32-bit words (4-byte aligned base and stride)
+  int32_t words;    // codes may be read as 32-bit words (4-byte aligned base and stride)
+  int32_t words16;  // table rows may be read as 16-byte words (16-byte aligned base and stride)
 };
 
 // PqAdcDistance for one code; `entry(s, c)` reads table[s * 256 + c].
@@ -261,12 +262,8 @@ __global__ __launch_bounds__(kThreads) void pq_adc_kernel(PqAdc p) {
 }
 
 // The ADC scan for codes of at most 32 bytes laid out on 16-byte boundaries
-// (base and stride): a code arrives in kChunks 16-byte loads, each lane
-// takes kAdcCodes codes per round and requests the next round's codes before
-// summing the current ones, and the table sits in LDS.  The sums are
-// adc_sum's, on the code's words.  (Two codes per round: four held 64 VGPRs
-// and ran slower at the lower occupancy.)
-constexpr int kAdcCodes = 2;
+// (base and stride): a code arrives in kChunks 16-byte loads, and the table
+// sits in LDS.  The sums are adc_sum's, on the code's words.
 
 template <int kChunks, typename Entry>
 __device__ __forceinline__ float adc_sum_words(const uint4 (&chunk)[kChunks], int m, Entry entry) {
@@ -302,61 +299,72 @@ __device__ __forceinline__ float adc_sum_words(const uint4 (&chunk)[kChunks], in
   return sum;
 }
 
-template <int kChunks>
-__global__ __launch_bounds__(kThreads) void pq_adc_vec_kernel(PqAdc p) {
+// Workgroups of the 16-byte ADC scan: 512 threads, four per compute unit
+// (kAdcBlocks over the 256 CUs of an MI355X), so the table is staged 1024
+// times per launch instead of once per 256 codes.
+constexpr int kAdcThreads = 512;
+constexpr int64_t kAdcBlocks = 1024;
+
+// Each lane sums one code per step and holds two steps' codes in two register
+// sets: the next step's code is requested before the current one is summed.
+// Every load is issued unconditionally (a candidate past the end re-reads the
+// last one, an id past the codes reads code 0, and both are masked after),
+// so the compiler can wait for exactly the older set with a counted
+// s_waitcnt; loads behind a branch, or a copy of one set into the other,
+// make it wait for every load in flight, the next step's included.  Codes are
+// read once and the distances written once: both bypass the caches
+// (non-temporal), and the table is staged with 16-byte loads where its rows
+// allow.  kM is the sub-space count when known at compile time (the engine's
+// 16: the lookups of a code are issued together), 0 for p.subspaces.  The
+// launch requires num_codes >= 1.
+template <int kChunks, int kM, bool kIds>
+__global__ __launch_bounds__(kAdcThreads) void pq_adc_vec_kernel(PqAdc p) {
   extern __shared__ float table_lds[];  // subspaces * 256 floats
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   const int64_t q = blockIdx.y;
   const float* table = p.tables + q * p.table_stride;
-  const int m = p.subspaces;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  // Codes base + k * stride, k < kAdcCodes: valid flags and 16-byte chunks.
-  auto load = [&](int64_t base, bool (&valid)[kAdcCodes], uint4 (&chunk)[kAdcCodes][kChunks]) {
-    // All candidate ids first, so their latencies overlap.
-    uint32_t id[kAdcCodes];
-#pragma unroll
-    for (int k = 0; k < kAdcCodes; ++k) {
-      const int64_t cand = base + k * stride;
-      id[k] = p.ids != nullptr && cand < p.num_cand ? p.ids[cand] : 0u;
+  const int m = kM > 0 ? kM : p.subspaces;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kAdcThreads;
+  const int64_t last = p.num_cand - 1;
+  // Candidate `cand`'s code into `chunk`; `valid` says whether it exists.
+  auto load = [&](int64_t cand, bool& valid, uint4 (&chunk)[kChunks]) {
+    const int64_t c = cand < last ? cand : last;
+    int64_t index = c;
+    valid = cand <= last;
+    if constexpr (kIds) {
+      const uint32_t id = p.ids[c];
+      valid = valid && static_cast<int64_t>(id) < p.num_codes;
+      index = valid ? static_cast<int64_t>(id) : 0;
     }
 #pragma unroll
-    for (int k = 0; k < kAdcCodes; ++k) {
-      const int64_t cand = base + k * stride;
-      int64_t index = cand;
-      valid[k] = cand < p.num_cand;
-      if (p.ids != nullptr) {
-        valid[k] = valid[k] && static_cast<int64_t>(id[k]) < p.num_codes;
-        index = id[k];
-      }
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c)
-        chunk[k][c] = valid[k] ? *reinterpret_cast<const uint4*>(p.codes + index * p.code_stride + 16 * c)
-                               : make_uint4(0, 0, 0, 0);
+    for (int k = 0; k < kChunks; ++k) {
+      const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.codes + index * p.code_stride + 16 * k));
+      chunk[k] = make_uint4(x[0], x[1], x[2], x[3]);
     }
   };
-  // The first codes are requested before the table is staged, and each
-  // round requests the next round's codes before summing its own.
-  int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  bool valid[kAdcCodes];
-  uint4 chunk[kAdcCodes][kChunks];
-  load(base, valid, chunk);
-  for (int i = static_cast<int>(threadIdx.x); i < m * VECTRA_PQ_CENTROIDS; i += kThreads) table_lds[i] = table[i];
+  // The first code is requested before the table is staged.
+  int64_t cand = static_cast<int64_t>(blockIdx.x) * kAdcThreads + threadIdx.x;
+  bool valid_a, valid_b;
+  uint4 chunk_a[kChunks], chunk_b[kChunks];
+  load(cand, valid_a, chunk_a);
+  if (p.words16 != 0) {
+    const uint4* t4 = reinterpret_cast<const uint4*>(table);
+    uint4* l4 = reinterpret_cast<uint4*>(table_lds);
+    for (int i = static_cast<int>(threadIdx.x); i < m * VECTRA_PQ_CENTROIDS / 4; i += kAdcThreads) l4[i] = t4[i];
+  } else {
+    for (int i = static_cast<int>(threadIdx.x); i < m * VECTRA_PQ_CENTROIDS; i += kAdcThreads) table_lds[i] = table[i];
+  }
   __syncthreads();
   auto entry = [&](int s, uint32_t c) { return table_lds[s * VECTRA_PQ_CENTROIDS + static_cast<int>(c)]; };
-  for (; base < p.num_cand; base += stride * kAdcCodes) {
-    bool next_valid[kAdcCodes];
-    uint4 next[kAdcCodes][kChunks];
-    load(base + stride * kAdcCodes, next_valid, next);
-#pragma unroll
-    for (int k = 0; k < kAdcCodes; ++k) {
-      const int64_t cand = base + k * stride;
-      if (cand < p.num_cand) p.out[q * p.out_stride + cand] = valid[k] ? adc_sum_words(chunk[k], m, entry) : NAN;
-    }
-#pragma unroll
-    for (int k = 0; k < kAdcCodes; ++k) {
-      valid[k] = next_valid[k];
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c) chunk[k][c] = next[k][c];
-    }
+  auto emit = [&](int64_t at, bool valid, const uint4 (&chunk)[kChunks]) {
+    const float d = valid ? adc_sum_words(chunk, m, entry) : NAN;
+    if (at <= last) __builtin_nontemporal_store(d, &p.out[q * p.out_stride + at]);
+  };
+  for (; cand <= last; cand += 2 * stride) {
+    load(cand + stride, valid_b, chunk_b);
+    emit(cand, valid_a, chunk_a);
+    load(cand + 2 * stride, valid_a, chunk_a);
+    emit(cand + stride, valid_b, chunk_b);
   }
 }
 
@@ -779,14 +787,22 @@ extern "C" int vectra_scan_pq_adc(const vectra_pq_adc_args* a, hipStream_t strea
   p.num_cand = cand;
   p.subspaces = a->subspaces;
   p.words = (a->code_stride % 4 == 0 && reinterpret_cast<uintptr_t>(a->codes) % 4 == 0) ? 1 : 0;
+  p.words16 = (a->table_stride % 4 == 0 && reinterpret_cast<uintptr_t>(a->tables) % 16 == 0) ? 1 : 0;
   void* args[] = {&p};
   const dim3 grid(blocks_for(cand, kThreads, kScanBlocks), static_cast<unsigned>(a->num_queries));
   const bool vec16 = a->code_stride % 16 == 0 && reinterpret_cast<uintptr_t>(a->codes) % 16 == 0;
-  if (vec16 && a->subspaces <= 32) {
+  if (vec16 && a->subspaces <= 32 && a->num_codes > 0) {
     const size_t lds = static_cast<size_t>(entries) * sizeof(float);
-    const void* kernel = a->subspaces <= 16 ? reinterpret_cast<const void*>(&pq_adc_vec_kernel<1>)
-                                            : reinterpret_cast<const void*>(&pq_adc_vec_kernel<2>);
-    return launched(hipLaunchKernel(kernel, grid, dim3(kThreads), args, lds, stream));
+    const bool ids = a->ids != nullptr;
+    const void* kernel =
+        a->subspaces == 16 ? (ids ? reinterpret_cast<const void*>(&pq_adc_vec_kernel<1, 16, true>)
+                                  : reinterpret_cast<const void*>(&pq_adc_vec_kernel<1, 16, false>))
+        : a->subspaces < 16 ? (ids ? reinterpret_cast<const void*>(&pq_adc_vec_kernel<1, 0, true>)
+                                   : reinterpret_cast<const void*>(&pq_adc_vec_kernel<1, 0, false>))
+                            : (ids ? reinterpret_cast<const void*>(&pq_adc_vec_kernel<2, 0, true>)
+                                   : reinterpret_cast<const void*>(&pq_adc_vec_kernel<2, 0, false>));
+    const dim3 vgrid(blocks_for(cand, kAdcThreads, kAdcBlocks), static_cast<unsigned>(a->num_queries));
+    return launched(hipLaunchKernel(kernel, vgrid, dim3(kAdcThreads), args, lds, stream));
   }
   if (a->subspaces <= kMaxLdsTableSubspaces) {
     const size_t lds = static_cast<size_t>(entries) * sizeof(float);
