@@ -282,7 +282,8 @@ def test_nearest_equals_the_reference_outputs(golden):
 @pytest.mark.parametrize('n,dim,k,queries', [(2048, 128, 10, 4), (2048, 128, 100, 2), (700, 17, 1, 3),
                                              (5000, 32, 1024, 2), (300, 300, 64, 2), (100, 0, 20, 2),
                                              (1, 8, 5, 1), (30, 16, 1024, 1), (300, 24, 16, 1100),
-                                             (2048, 128, 10, 1024)])
+                                             (2048, 128, 10, 1024), (5000, 128, 1024, 2), (2999, 128, 7, 1030),
+                                             (3001, 128, 64, 3)])
 def test_nearest_against_the_oracle(n, dim, k, queries):
     rng = np.random.default_rng(n + dim + k)
     rows = rng.standard_normal((n, dim)).astype(np.float32)
@@ -292,9 +293,11 @@ def test_nearest_against_the_oracle(n, dim, k, queries):
     _check_nearest(q, rows, k, msg=f'n={n} dim={dim} k={k}')
 
 
-def test_nearest_with_candidate_ids_and_special_values():
+# 128-dimensional rows take the pipelined kernels (two register sets of rows).
+@pytest.mark.parametrize('dim', [40, 128])
+def test_nearest_with_candidate_ids_and_special_values(dim):
     rng = np.random.default_rng(3)
-    n, dim = 900, 40
+    n = 900
     rows = rng.standard_normal((n, dim)).astype(np.float32)
     rows[5, 3] = np.nan     # a NaN distance: after every number
     rows[6, 0] = np.inf     # an infinite distance
@@ -304,18 +307,19 @@ def test_nearest_with_candidate_ids_and_special_values():
     ids[:100] = ids[100:200]                                # duplicates: kept
     ids[200:203] = [5, 6, 7]
     for k in (1, 16, 257, 1024):
-        print(f'nearest ids k={k}', flush=True)
-        _check_nearest(q, rows, k, ids, msg=f'ids k={k}')
+        print(f'nearest ids dim={dim} k={k}', flush=True)
+        _check_nearest(q, rows, k, ids, msg=f'ids dim={dim} k={k}')
     # A query equal to a row: distance exactly 0 first.
     q2 = rows[[11]].copy()
     d, nodes = scan.nearest(_gpu(q2), _gpu(rows), 3)
     assert d[0, 0].item() == 0.0 and nodes[0, 0].item() == 11
 
 
-def test_nearest_keeps_up_when_every_candidate_is_better():
+@pytest.mark.parametrize('dim', [16, 128])
+def test_nearest_keeps_up_when_every_candidate_is_better(dim):
     """Distances falling with the row index: every candidate beats the k-th
     best so far, so the kernel merges its buffer again and again."""
-    dim, n, k = 16, 6000, 1024
+    n, k = 6000, 1024
     rng = np.random.default_rng(9)
     q = rng.standard_normal((1, dim)).astype(np.float32)
     u = np.zeros(dim, np.float32)
@@ -332,14 +336,15 @@ def test_nearest_over_a_large_shard():
     _check_nearest(q, rows, 10, msg='200k rows')
 
 
+@pytest.mark.parametrize('dim', [24, 128])
 @pytest.mark.parametrize('valid', [0, 7, 90])
-def test_split_ranges_with_few_or_no_valid_candidates(valid):
+def test_split_ranges_with_few_or_no_valid_candidates(valid, dim):
     """Ranges whose candidates are mostly (or all) ids past the row count:
     their lists end in empty slots, and the merge must still return exactly
     the valid candidates, then +inf and NO_NODE."""
     rng = np.random.default_rng(50 + valid)
-    rows = rng.standard_normal((100, 24)).astype(np.float32)
-    q = rng.standard_normal((2, 24)).astype(np.float32)
+    rows = rng.standard_normal((100, dim)).astype(np.float32)
+    q = rng.standard_normal((2, dim)).astype(np.float32)
     ids = rng.integers(100, 1000, 300).astype(np.uint32)  # past the rows: skipped
     ids[rng.choice(300, valid, replace=False)] = rng.integers(0, 100, valid)
     for k in (10, 64, 100):
@@ -348,21 +353,22 @@ def test_split_ranges_with_few_or_no_valid_candidates(valid):
         _check_nearest(q, rows, k, ids, msg=f'valid={valid} k={k}')
 
 
+@pytest.mark.parametrize('dim', [32, 128])
 @pytest.mark.parametrize('k,length,skipped', [(1000, 1030, 30), (993, 1031, 32), (1024, 1060, 20)])
-def test_split_range_merged_on_overflow_below_k(k, length, skipped):
+def test_split_range_merged_on_overflow_below_k(k, length, skipped, dim):
     """A range whose buffer overflows while it holds fewer than k keys (ids
     past the row count skipped among its first 1024 candidates), then a short
     last round: the range's earlier keys must survive the last selection
     (tests/topk_model.py names the case).  Two ranges of `length` ids; every
     form, no_alloc included, against the oracle."""
     rng = np.random.default_rng(k + skipped)
-    n_rows, dim = 3000, 32
+    n_rows = 3000
     rows = rng.standard_normal((n_rows, dim)).astype(np.float32)
     q = rng.standard_normal((1, dim)).astype(np.float32)
     ids = rng.integers(0, n_rows, 2 * length).astype(np.uint32)
     ids[rng.choice(1024, size=skipped, replace=False)] = n_rows + rng.integers(0, 500, skipped)
     assert scan.workspace_bytes(_gpu(q), _gpu(rows), k, _gpu(ids)) > 0  # the split form is taken
-    print(f'split overflow below k: k={k} ids={2 * length} skipped={skipped}', flush=True)
+    print(f'split overflow below k: dim={dim} k={k} ids={2 * length} skipped={skipped}', flush=True)
     _check_nearest(q, rows, k, ids, msg=f'overflow k={k}')
 
 

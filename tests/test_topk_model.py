@@ -25,7 +25,7 @@ def _case(rng, n, k, skip_frac, descending=False, dup_frac=0.0):
     return model.candidate_keys(d, nodes, valid)
 
 
-@pytest.mark.parametrize('form', ['split', 'narrow', 'wide'])
+@pytest.mark.parametrize('form', ['split', 'narrow', 'wide', 'wide128'])
 @pytest.mark.parametrize('k', [1, 10, 64, 65, 500, 993, 1000, 1024])
 def test_the_selection_keeps_the_k_smallest(form, k):
     rng = np.random.default_rng(k * 7 + len(form))
@@ -70,7 +70,7 @@ def test_only_the_split_form_takes_the_one_wave_first_selection():
     # Rounds of 256 and 384 always merge (keys[0 .. k) in the sort), so the
     # emptiness rule cannot matter there.
     keys = _overflow_case(1000, 1030, 30)
-    for form in ('narrow', 'wide'):
+    for form in ('narrow', 'wide', 'wide128'):
         want = model.sorted_k(keys, 1000)
         np.testing.assert_array_equal(model.top_k(keys, 1000, form, empty_test='worst'), want)
 

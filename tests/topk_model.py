@@ -39,7 +39,8 @@ WAVE = 64                        # kWaveLanes
 FORMS = {
     'split': (256, 4, 1),      # the split form (vectra_scan_top_k_ws / no_alloc)
     'narrow': (256, 4, 4),     # 1024 queries or more
-    'wide': (1024, 6, 1),      # fewer queries, one workgroup each
+    'wide': (1024, 6, 1),      # fewer queries, one workgroup each (any dimension)
+    'wide128': (1024, 4, 1),   # the same for 128-dimensional rows (the pipelined kernel)
 }
 
 

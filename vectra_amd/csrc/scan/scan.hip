@@ -485,9 +485,12 @@ __device__ __forceinline__ uint64_t wave_min(uint64_t key) {
 }
 
 // kTopKThreads threads; a 16-lane group loads kTopKCands candidates at once,
-// kSteps times per round of candidates between merge checks.
-template <bool kIds, int kTopKThreads, int kTopKCands, int kSteps>
+// kSteps times per round of candidates between merge checks.  kDim is the
+// row dimension when known at compile time (a multiple of 16 up to 128: the
+// engine's 128), 0 for p.dim.
+template <bool kIds, int kTopKThreads, int kTopKCands, int kSteps, int kDim = 0>
 __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
+  static_assert(kDim % 16 == 0 && kDim <= 128, "whole 16-element steps, one unrolled pass");
   constexpr int kTopKGroups = kTopKThreads / kLanes;
   constexpr int kTopKRound = kTopKGroups * kTopKCands * kSteps;
   static_assert(kTopKKeys - VECTRA_SCAN_MAX_K >= kTopKRound, "room for a round of candidates");
@@ -562,76 +565,149 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
   // than k keys (ids past the rows are skipped), which leaves `worst` empty
   // with keys in the buffer, so `worst` cannot tell an empty buffer.
   bool selected = false;
-  for (int64_t base = cand_begin; base < cand_end; base += kTopKRound) {
-    // A round: kSteps steps of kTopKCands candidates per 16-lane group, a
-    // step's loads issued before any of its sums (each candidate's own
-    // operations keep the row scan's order).
-    for (int s = 0; s < kSteps; ++s) {
-      bool valid[kTopKCands];
-      const float* rlane[kTopKCands];
-      int64_t row[kTopKCands];
-#pragma unroll
-      for (int c = 0; c < kTopKCands; ++c) {
-        const int64_t cand = base + static_cast<int64_t>(s * kTopKCands + c) * kTopKGroups + group;
-        valid[c] = cand < cand_end;
-        row[c] = valid[c] ? cand : 0;
-        if constexpr (kIds) {
-          const uint32_t id = valid[c] ? p.ids[cand] : 0u;
-          valid[c] = valid[c] && static_cast<int64_t>(id) < p.num_rows;
-          row[c] = valid[c] ? id : 0;
-        }
-        rlane[c] = p.rows + row[c] * p.row_stride + lane;
-      }
-      float acc[kTopKCands];
-#pragma unroll
-      for (int c = 0; c < kTopKCands; ++c) acc[c] = 0.f;
-      int i = 0;
-      for (; i + kLanes * kUnroll <= full; i += kLanes * kUnroll) {
-        float rv[kTopKCands][kUnroll], qv[kUnroll];
-#pragma unroll
-        for (int c = 0; c < kTopKCands; ++c)
-#pragma unroll
-          for (int u = 0; u < kUnroll; ++u) rv[c][u] = valid[c] ? rlane[c][i + kLanes * u] : 0.f;
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) qv[u] = qlane[i + kLanes * u];
-#pragma unroll
-        for (int c = 0; c < kTopKCands; ++c)
-#pragma unroll
-          for (int u = 0; u < kUnroll; ++u) acc[c] = acc[c] + term<VECTRA_SCAN_L2_SQUARED>(qv[u], rv[c][u]);
-      }
-      for (; i < full; i += kLanes) {
-        const float qi = qlane[i];
-#pragma unroll
-        for (int c = 0; c < kTopKCands; ++c)
-          acc[c] = acc[c] + term<VECTRA_SCAN_L2_SQUARED>(qi, valid[c] ? rlane[c][i] : 0.f);
-      }
-#pragma unroll
-      for (int c = 0; c < kTopKCands; ++c) {
-        float sum = acc[c];
-#pragma unroll
-        for (int width = kLanes / 2; width > 0; width /= 2) {
-          const float other = __shfl_down(sum, width, kLanes);
-          if (lane < width) sum = sum + other;
-        }
-        float t = 0.f;
-        if (valid[c] && lane < tail) t = term<VECTRA_SCAN_L2_SQUARED>(qlane[full], rlane[c][full]);
-        for (int e = 0; e < tail; ++e) sum = sum + __shfl(t, e, kLanes);
-        if (valid[c] && lane == 0) {
-          const uint64_t key = nearest_key(sum, static_cast<uint32_t>(row[c]));
-          if (key < worst) keys[k + atomicAdd(&fill, 1u)] = key;
-        }
-      }
-    }
+  // End of a round: merge once k candidates are in hand (the threshold then
+  // discards most of the rest), and whenever the next round might not fit.
+  auto round_end = [&]() {
     __syncthreads();
     const int n = static_cast<int>(fill);
-    // Merge once k candidates are in hand (the threshold then discards most
-    // of the rest), and whenever the next round might not fit.
     if ((worst == kNoKey && n >= k) || n > kTopKKeys - k - kTopKRound) {
       select(!selected, n);
       selected = true;
       if (tid == 0) fill = 0;
       worst = keys[k - 1];
       __syncthreads();
+    }
+  };
+  if constexpr (kDim > 0) {
+    // Steps of kTopKCands candidates per group, in two register sets: the
+    // next step's rows are requested before the current step is summed, and
+    // the next round's first step before a round's merge.  Every load is
+    // issued (a candidate past the range re-reads the range's first, an id
+    // past the rows reads row 0, and both are masked), so the compiler waits
+    // for exactly the older set.  The query's kDim / 16 elements of this
+    // lane stay in registers.  Each candidate's operations are the row
+    // scan's, in its order.
+    constexpr int kPer = kDim / kLanes;
+    struct Step {
+      float v[kTopKCands][kPer];
+      uint32_t row[kTopKCands];
+      bool ok[kTopKCands];
+    };
+    float qv[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) qv[u] = qlane[kLanes * u];
+    const int64_t len = cand_end - cand_begin;
+    const int64_t steps = p.num_rows > 0 && len > 0 ? (len + kTopKRound - 1) / kTopKRound * kSteps : 0;
+    auto load = [&](int64_t t, Step& st) {
+      const int64_t first = cand_begin + (t / kSteps) * kTopKRound + (t % kSteps) * (kTopKCands * kTopKGroups);
+#pragma unroll
+      for (int c = 0; c < kTopKCands; ++c) {
+        const int64_t cand = first + c * kTopKGroups + group;
+        bool ok = cand < cand_end;
+        int64_t row = ok ? cand : cand_begin;
+        if constexpr (kIds) {
+          const uint32_t id = p.ids[row];
+          ok = ok && static_cast<int64_t>(id) < p.num_rows;
+          row = ok ? id : 0;
+        }
+        st.ok[c] = ok;
+        st.row[c] = static_cast<uint32_t>(row);
+        const float* r = p.rows + row * p.row_stride + lane;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) st.v[c][u] = r[kLanes * u];
+      }
+    };
+    auto consume = [&](const Step& st) {
+#pragma unroll
+      for (int c = 0; c < kTopKCands; ++c) {
+        float sum = 0.f;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) sum = sum + term<VECTRA_SCAN_L2_SQUARED>(qv[u], st.v[c][u]);
+#pragma unroll
+        for (int width = kLanes / 2; width > 0; width /= 2) {
+          const float other = __shfl_down(sum, width, kLanes);
+          if (lane < width) sum = sum + other;
+        }
+        if (st.ok[c] && lane == 0) {
+          const uint64_t key = nearest_key(sum, st.row[c]);
+          if (key < worst) keys[k + atomicAdd(&fill, 1u)] = key;
+        }
+      }
+    };
+    Step a, b;
+    if (steps > 0) load(0, a);
+    for (int64_t t = 0; t < steps; t += 2) {
+      load(t + 1 < steps ? t + 1 : t, b);
+      consume(a);
+      if ((t + 1) % kSteps == 0) round_end();
+      load(t + 2 < steps ? t + 2 : t, a);
+      if (t + 1 < steps) {
+        consume(b);
+        if ((t + 2) % kSteps == 0) round_end();
+      }
+    }
+  } else {
+    for (int64_t base = cand_begin; base < cand_end; base += kTopKRound) {
+      // A round: kSteps steps of kTopKCands candidates per 16-lane group, a
+      // step's loads issued before any of its sums (each candidate's own
+      // operations keep the row scan's order).
+      for (int s = 0; s < kSteps; ++s) {
+        bool valid[kTopKCands];
+        const float* rlane[kTopKCands];
+        int64_t row[kTopKCands];
+#pragma unroll
+        for (int c = 0; c < kTopKCands; ++c) {
+          const int64_t cand = base + static_cast<int64_t>(s * kTopKCands + c) * kTopKGroups + group;
+          valid[c] = cand < cand_end;
+          row[c] = valid[c] ? cand : 0;
+          if constexpr (kIds) {
+            const uint32_t id = valid[c] ? p.ids[cand] : 0u;
+            valid[c] = valid[c] && static_cast<int64_t>(id) < p.num_rows;
+            row[c] = valid[c] ? id : 0;
+          }
+          rlane[c] = p.rows + row[c] * p.row_stride + lane;
+        }
+        float acc[kTopKCands];
+#pragma unroll
+        for (int c = 0; c < kTopKCands; ++c) acc[c] = 0.f;
+        int i = 0;
+        for (; i + kLanes * kUnroll <= full; i += kLanes * kUnroll) {
+          float rv[kTopKCands][kUnroll], qv[kUnroll];
+#pragma unroll
+          for (int c = 0; c < kTopKCands; ++c)
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) rv[c][u] = valid[c] ? rlane[c][i + kLanes * u] : 0.f;
+#pragma unroll
+          for (int u = 0; u < kUnroll; ++u) qv[u] = qlane[i + kLanes * u];
+#pragma unroll
+          for (int c = 0; c < kTopKCands; ++c)
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) acc[c] = acc[c] + term<VECTRA_SCAN_L2_SQUARED>(qv[u], rv[c][u]);
+        }
+        for (; i < full; i += kLanes) {
+          const float qi = qlane[i];
+#pragma unroll
+          for (int c = 0; c < kTopKCands; ++c)
+            acc[c] = acc[c] + term<VECTRA_SCAN_L2_SQUARED>(qi, valid[c] ? rlane[c][i] : 0.f);
+        }
+#pragma unroll
+        for (int c = 0; c < kTopKCands; ++c) {
+          float sum = acc[c];
+#pragma unroll
+          for (int width = kLanes / 2; width > 0; width /= 2) {
+            const float other = __shfl_down(sum, width, kLanes);
+            if (lane < width) sum = sum + other;
+          }
+          float t = 0.f;
+          if (valid[c] && lane < tail) t = term<VECTRA_SCAN_L2_SQUARED>(qlane[full], rlane[c][full]);
+          for (int e = 0; e < tail; ++e) sum = sum + __shfl(t, e, kLanes);
+          if (valid[c] && lane == 0) {
+            const uint64_t key = nearest_key(sum, static_cast<uint32_t>(row[c]));
+            if (key < worst) keys[k + atomicAdd(&fill, 1u)] = key;
+          }
+        }
+      }
+      round_end();
     }
   }
   const int n = static_cast<int>(fill);
@@ -890,20 +966,26 @@ int64_t top_k_workspace(int64_t queries, int64_t splits, int k) {
   return splits > 1 ? kCounterBytes + queries * splits * k * int64_t{8} : 0;
 }
 
+// The kernel of a launch form, for ids or none.
+template <int kThreadsT, int kCands, int kSteps, int kDim>
+const void* top_k_kernel(bool ids) {
+  return ids ? reinterpret_cast<const void*>(&scan_top_k_kernel<true, kThreadsT, kCands, kSteps, kDim>)
+             : reinterpret_cast<const void*>(&scan_top_k_kernel<false, kThreadsT, kCands, kSteps, kDim>);
+}
+
+// The engine's 128 dimensions take the pipelined kernels.  (Six candidates
+// per group in the wide form's generic kernel; four in its pipelined one,
+// whose two register sets hold six only with spills.)
 int launch_top_k(int64_t queries, TopK& p, hipStream_t stream) {
   void* args[] = {&p};
-  if (p.splits > 1) {
-    const void* kernel = p.ids != nullptr ? reinterpret_cast<const void*>(&scan_top_k_kernel<true, 256, 4, 1>)
-                                          : reinterpret_cast<const void*>(&scan_top_k_kernel<false, 256, 4, 1>);
-    return launched(hipLaunchKernel(kernel, dim3(static_cast<unsigned>(queries * p.splits)), dim3(256), args, 0,
-                                    stream));
-  }
+  const bool ids = p.ids != nullptr;
+  const bool d128 = p.dim == 128;
+  if (p.splits > 1)
+    return launched(hipLaunchKernel(d128 ? top_k_kernel<256, 4, 1, 128>(ids) : top_k_kernel<256, 4, 1, 0>(ids),
+                                    dim3(static_cast<unsigned>(queries * p.splits)), dim3(256), args, 0, stream));
   const bool wide = queries < kTopKWideBelow;
-  const void* kernel = p.ids != nullptr
-                           ? (wide ? reinterpret_cast<const void*>(&scan_top_k_kernel<true, 1024, 6, 1>)
-                                   : reinterpret_cast<const void*>(&scan_top_k_kernel<true, 256, 4, 4>))
-                           : (wide ? reinterpret_cast<const void*>(&scan_top_k_kernel<false, 1024, 6, 1>)
-                                   : reinterpret_cast<const void*>(&scan_top_k_kernel<false, 256, 4, 4>));
+  const void* kernel = wide ? (d128 ? top_k_kernel<1024, 4, 1, 128>(ids) : top_k_kernel<1024, 6, 1, 0>(ids))
+                            : (d128 ? top_k_kernel<256, 4, 4, 128>(ids) : top_k_kernel<256, 4, 4, 0>(ids));
   return launched(hipLaunchKernel(kernel, dim3(static_cast<unsigned>(queries)), dim3(wide ? 1024 : 256), args, 0,
                                   stream));
 }
