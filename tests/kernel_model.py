@@ -56,7 +56,9 @@ F32 = np.float32
 LOG2E = F32(1.4426950408889634)
 TWO_LOG2E = F32(2.0) * LOG2E
 SUM_RANGE = {'bf16': (F32(2.0 ** -32), F32(2.0 ** 32)), 'fp16': (F32(2.0 ** -3), F32(2.0 ** 15))}
-TILE_ITEM_ROWS = 128  # query rows of one tile-kernel work item (4 waves x 2 blocks x 16)
+# Query rows of one tile-kernel work item, by head dim: 4 waves x blocks of 16
+# per wave (four blocks for 64-dim heads, two otherwise).
+TILE_ITEM_ROWS = {32: 128, 64: 256, 128: 128}
 FAST_KEYS = 1024      # the tile kernel tries its fast pass from this many keys
 FAST_SUM = F32(256)   # and keeps it if every weight sum of the item is at least this
 FAST_SIGMAS = 4.0     # and this many deviations of its rounding walk fit the contract
@@ -207,7 +209,7 @@ def plane(q, k, v, gamma, bias, kind, one_pass=False):
 
 
 def tile(q, k, v, gamma, bias, kind, one_pass=False, split_weights=False):
-    """rbf_tile_kernel on one plane (work items of 128 query rows); same
+    """rbf_tile_kernel on one plane (work items of TILE_ITEM_ROWS query rows); same
     arguments as `plane`, paths SPLIT, SHIFTED or FAST.  `one_pass` models
     the split pass alone (no fast pass, no recompute); `split_weights` the
     VECTRA_FLAG_SPLIT_WEIGHTS flag (no fast pass)."""
@@ -223,8 +225,9 @@ def tile(q, k, v, gamma, bias, kind, one_pass=False, split_weights=False):
     if fast:
         with np.errstate(over='ignore'):
             v16 = v.astype(np.float16).astype(F32)  # exact for fp16 inputs
-    for r0 in range(0, nq, TILE_ITEM_ROWS):
-        rows = slice(r0, min(r0 + TILE_ITEM_ROWS, nq))
+    item_rows = TILE_ITEM_ROWS.get(q.shape[1], 128)
+    for r0 in range(0, nq, item_rows):
+        rows = slice(r0, min(r0 + item_rows, nq))
         x0 = fma32(coef, s[rows], c[None, :])
         if fast:
             acc, total, kept = fast_pass(x0, v16, k.shape[0], TILE_KEYS.get(q.shape[1], 64))

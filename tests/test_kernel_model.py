@@ -162,10 +162,10 @@ def test_dropping_the_clamp_costs_no_more_than_the_expansion_error(kind, norm, g
 
 # The tile kernel's fast pass (fp16 weights, no split) on long key axes.
 
-def _long_keys(seed, kind, n_k=1280, n_q=160, dim=64, gamma=0.03, v_scale=0.25):
+def _long_keys(seed, kind, n_k=1280, n_q=320, dim=64, gamma=0.03, v_scale=0.25):
     """A plane like config 4's (q, k ~ 0.5 N(0, 1)) with values v_scale N(0, 1)
-    and a key axis long enough for the fast pass; 160 queries are two work
-    items.  (At 1280 keys the fast pass holds for values of a quarter of
+    and a key axis long enough for the fast pass; 320 queries are two work
+    items of 64-dim heads (256 and 64 rows).  (At 1280 keys the fast pass holds for values of a quarter of
     config 4's; config 4's own values need its 4096 keys.)"""
     gen = torch.Generator().manual_seed(seed)
     q = 0.5 * torch.randn(1, 1, n_q, dim, generator=gen)
@@ -204,11 +204,12 @@ def test_the_fast_pass_runs_where_it_holds(kind):
     # Weight sums below FAST_SUM (a large gamma) send the item to the split.
     assert (km.run('tile', q, k, v, torch.tensor(0.3), bias, kind)[1] != km.FAST).all()
     # Per work item: queries far from the keys in the second item only.
+    item = km.TILE_ITEM_ROWS[64]
     far = q.clone()
-    far[..., 128:, :] += 1.5
+    far[..., item:, :] += 1.5
     far = far.to(KINDS[kind]).float()
     path = km.run('tile', far, k, v, scale, bias, kind)[1][0, 0]
-    assert (path[:128] == km.FAST).all() and (path[128:] != km.FAST).all()
+    assert (path[:item] == km.FAST).all() and (path[item:] != km.FAST).all()
     # Values 16 times larger: the bound misses the contract, the item splits.
     big = (v * 16).to(KINDS[kind]).float()
     assert (km.run('tile', q, k, big, scale, bias, kind)[1] == km.SPLIT).all()
@@ -225,7 +226,7 @@ def test_values_fp16_cannot_hold_send_the_item_to_the_split():
 
 def _config4_plane(seed, kind, gamma, v_scale, n_q=128):
     """One plane of config 4 (q, k ~ 0.5 N(0, 1), v ~ N(0, 1), 4096 keys of 64
-    dims), one work item of queries, values scaled by v_scale."""
+    dims), 128 queries (part of one work item), values scaled by v_scale."""
     return _long_keys(seed, kind, n_k=4096, n_q=n_q, gamma=gamma, v_scale=v_scale)
 
 

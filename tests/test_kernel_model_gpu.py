@@ -78,11 +78,12 @@ def _long_key_cases(kind):
     """Long key axes through each of the tile kernel's paths: (name, inputs,
     split_weights flag, number of leading queries on the fast pass)."""
     q, k, v, scale, bias = _long_keys(1, kind)
+    item = km.TILE_ITEM_ROWS[64]
     far = q.clone()
-    far[..., 128:, :] += 1.5
+    far[..., item:, :] += 1.5
     far = far.to(KINDS[kind]).float()  # the model takes the inputs the kernel sees
-    yield 'fast', (q, k, v, scale, bias), False, 160
-    yield 'second_item_below_the_guard', (far, k, v, scale, bias), False, 128
+    yield 'fast', (q, k, v, scale, bias), False, q.shape[2]
+    yield 'second_item_below_the_guard', (far, k, v, scale, bias), False, item
     yield 'large_gamma', (q, k, v, torch.tensor(0.3), bias), False, 0
     yield 'few_live_keys', _concentrated(16, 16, kind), False, 0
     yield 'bound_edge', _concentrated(0, 380, kind), False, 0

@@ -37,7 +37,7 @@ bool tile_supports(const Problem& p, int in_dtype, int out_dtype) {
   if (p.so[2] < 0 || p.so[3] < 0 ||
       ((p.Nq - 1) * p.so[2] + (p.Dv - 1) * p.so[3]) * out_size + out_size - 1 > kMax32)
     return false;
-  // Work items (planes x blocks of 128 query rows) and item + grid size are 32-bit.
+  // Work items (planes x blocks of at least 128 query rows) and item + grid size are 32-bit.
   return p.B * p.H * ((p.Nq + 127) / 128) < (int64_t{1} << 30);
 }
 

@@ -11,7 +11,7 @@
 //
 // with the lane layouts of rbf_mfma_ops.h.  A K fragment read from LDS feeds
 // the products of every query block of the wave, and so does a V^T fragment:
-// two blocks per wave halve the LDS traffic per product.
+// two blocks per wave halve the LDS traffic per product, four quarter it.
 //
 // Per-score arithmetic is one FMA, one exp2 and the 16-bit split of the
 // weight:
@@ -132,10 +132,13 @@ constexpr float kFastSigmas = 4.f;
 constexpr float kGateAtol = 1e-4f, kGateRtol = 1e-3f;
 constexpr float kFastWalk = kFastSigmas * 0x1p-11f * 0.57735026919f;  // kFastSigmas 2^-11 / sqrt(3)
 
-// Three waves per SIMD (at most 168 VGPRs) measured fastest for head dims
-// up to 64; 128-dim heads keep two.
+// Two query blocks per wave at three waves per SIMD (at most 168 VGPRs)
+// for 32-dim heads; four blocks at two waves per SIMD for 64-dim heads (each
+// K and V^T fragment, and each tile's staging, then serve 64 queries per
+// wave: 10 % faster at config 4 than two blocks at three waves); 128-dim
+// heads keep two blocks at two waves.
 template <typename T, typename OutT, int kD, int kKeys, int kWaves, int kCB>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kD <= 64 ? 3 : 2))) void
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kD <= 64 && kCB <= 2 ? 3 : 2))) void
 rbf_tile_kernel(Problem p, int32_t q_blocks) {
   using G = TileGeo<T, kD, kKeys, kWaves, kCB>;
   using Ops = MfmaOps<T>;
@@ -304,7 +307,7 @@ rbf_tile_kernel(Problem p, int32_t q_blocks) {
   // the diagonal holds every query's sum of squared weights.
   f32x4 wsq[kCB];
 
-  // Reduces tile `buf` for the wave's 32 queries.
+  // Reduces tile `buf` for the wave's 16 * kCB queries.
   auto compute = [&](int buf, float coef, auto kind_c) {
     constexpr int kind = decltype(kind_c)::value;
     const T* kl = reinterpret_cast<const T*>(lds + buf * G::kBufBytes);
@@ -663,7 +666,7 @@ template <typename T, typename OutT>
 hipError_t launch_tile_t(Problem& p, hipStream_t s) {
   switch (p.D) {
     case 32: return launch_tile_k<T, OutT, 32, 64, 4, 2>(p, s);
-    case 64: return launch_tile_k<T, OutT, 64, 64, 4, 2>(p, s);
+    case 64: return launch_tile_k<T, OutT, 64, 64, 4, 4>(p, s);
     case 128: return launch_tile_k<T, OutT, 128, 32, 4, 2>(p, s);
     default: return hipErrorInvalidValue;
   }
