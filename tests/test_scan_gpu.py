@@ -227,6 +227,24 @@ def test_tables_against_the_oracle(dim, m):
     _same(got, want, f'tables dim {dim} m {m}')
 
 
+@pytest.mark.parametrize('dim,m', [(128, 16), (64, 16), (256, 16), (512, 16), (96, 32)])
+def test_tables_for_many_queries_with_strides(dim, m):
+    # Blocks of 16 queries per workgroup (sub-vectors of 4, 8, 16 or 32
+    # floats), a last block of 5, queries and tables with row padding.
+    rng = np.random.default_rng(dim + 7 * m)
+    n_q = 37
+    books = rng.standard_normal((m, 256, dim // m)).astype(np.float32)
+    wide_q = _gpu(rng.standard_normal((n_q, dim + 3)).astype(np.float32))
+    queries = wide_q[:, 2:2 + dim]
+    out = torch.full((n_q, m * 256 + 9), 7.0, device='cuda')
+    got = scan.pq_distance_tables(queries, _gpu(books), m, out=out[:, :m * 256])
+    q_np = queries.cpu().numpy()
+    want = np.stack([oracle.pq_distance_table(q_np[i], books, m) for i in range(n_q)])
+    print(f'tables dim {dim} m {m} queries {n_q}', flush=True)
+    _same(got, want, f'tables dim {dim} m {m}')
+    assert (out[:, m * 256:] == 7.0).all()
+
+
 def test_tables_then_adc_rank_like_the_reference_search():
     # ComputeDistanceTable then PqAdcDistance over every code, as
     # engine/tests/tools/index_study.cc:79-83 does per query.

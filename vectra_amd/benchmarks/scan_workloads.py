@@ -90,7 +90,7 @@ WORKLOADS = {w.name: w for w in (
 )}
 
 # The kernel each workload runs (pq_shard's 16-byte codes take the 16-byte-load ADC kernel).
-KERNEL_NAMES = {'rows': 'scan_rows_kernel', 'adc': 'pq_adc_vec_kernel', 'tables': 'pq_table_kernel',
+KERNEL_NAMES = {'rows': 'scan_rows_kernel', 'adc': 'pq_adc_vec_kernel', 'tables': 'pq_table_sub_kernel',
                 'topk': 'scan_top_k_kernel'}
 VALU_LANE_OPS_PER_S = 256 * 4 * 16 * 2.4e9  # MI355X vector units, unpacked fp32
 

@@ -157,10 +157,36 @@ struct PqTable {
   float* tables;
   int64_t query_stride, table_stride, total;  // total = num_queries * subspaces * 256
   int32_t subspaces, dsub;
+  int32_t num_queries;
 };
 
-// One lane per table entry: L2SquaredDistance(sub-vector, centroid, dsub)
-// with the reference's sixteen accumulators held in registers.
+// L2SquaredDistance(sub-vector, centroid, dsub) with the reference's sixteen
+// accumulators held in registers.  kDsub is the sub-vector length when known
+// at compile time, 0 for `dsub`: with a constant length every load of the
+// operands is issued before the first term, where a loop of unknown length
+// waits for each load in turn.
+template <int kDsub>
+__device__ __forceinline__ float table_entry(const float* sub, const float* centroid, int dsub_rt) {
+  const int dsub = kDsub > 0 ? kDsub : dsub_rt;
+  float lanes[kLanes];
+#pragma unroll
+  for (int j = 0; j < kLanes; ++j) lanes[j] = 0.f;
+  const int full = dsub - dsub % kLanes;
+  for (int i = 0; i < full; i += kLanes) {
+#pragma unroll
+    for (int j = 0; j < kLanes; ++j) lanes[j] = lanes[j] + term<VECTRA_SCAN_L2_SQUARED>(sub[i + j], centroid[i + j]);
+  }
+#pragma unroll
+  for (int width = kLanes / 2; width > 0; width /= 2) {
+#pragma unroll
+    for (int j = 0; j < width; ++j) lanes[j] = lanes[j] + lanes[j + width];
+  }
+  float sum = lanes[0];
+  for (int i = full; i < dsub; ++i) sum = sum + term<VECTRA_SCAN_L2_SQUARED>(sub[i], centroid[i]);
+  return sum;
+}
+
+// One lane per table entry, any sub-vector length.
 __global__ __launch_bounds__(kThreads) void pq_table_kernel(PqTable p) {
   // total < 2^31 (checked on the host): 32-bit index arithmetic.
   for (uint32_t t = blockIdx.x * kThreads + threadIdx.x; t < static_cast<uint32_t>(p.total); t += gridDim.x * kThreads) {
@@ -170,23 +196,37 @@ __global__ __launch_bounds__(kThreads) void pq_table_kernel(PqTable p) {
     const int64_t q = qs / static_cast<uint32_t>(p.subspaces);
     const float* sub = p.queries + q * p.query_stride + static_cast<int64_t>(s) * p.dsub;
     const float* centroid = p.codebooks + (static_cast<int64_t>(s) * VECTRA_PQ_CENTROIDS + c) * p.dsub;
-    float lanes[kLanes];
-#pragma unroll
-    for (int j = 0; j < kLanes; ++j) lanes[j] = 0.f;
-    const int full = p.dsub - p.dsub % kLanes;
-    for (int i = 0; i < full; i += kLanes) {
-#pragma unroll
-      for (int j = 0; j < kLanes; ++j) lanes[j] = lanes[j] + term<VECTRA_SCAN_L2_SQUARED>(sub[i + j], centroid[i + j]);
-    }
-#pragma unroll
-    for (int width = kLanes / 2; width > 0; width /= 2) {
-#pragma unroll
-      for (int j = 0; j < width; ++j) lanes[j] = lanes[j] + lanes[j + width];
-    }
-    float sum = lanes[0];
-    for (int i = full; i < p.dsub; ++i) sum = sum + term<VECTRA_SCAN_L2_SQUARED>(sub[i], centroid[i]);
-    p.tables[q * p.table_stride + static_cast<int64_t>(s) * VECTRA_PQ_CENTROIDS + c] = sum;
+    p.tables[q * p.table_stride + static_cast<int64_t>(s) * VECTRA_PQ_CENTROIDS + c] = table_entry<0>(sub, centroid, p.dsub);
   }
+}
+
+// Sub-vectors of a known length up to 32: a workgroup of 256 lanes per
+// (block of kTableQueries queries, sub-space), lane c holding centroid c of
+// the sub-space in registers for every query of the block, the queries'
+// sub-vectors staged in LDS.  Each centroid is read once per block instead
+// of once per query, and the tables, written once, bypass the caches
+// (blocks of 8 queries measured fastest: 4.5 us at 1,024 queries, against
+// 4.7 with 16 and 5.3 with 4; cached stores 6.4 with 16).
+constexpr int kTableQueries = 8;
+
+template <int kDsub>
+__global__ __launch_bounds__(VECTRA_PQ_CENTROIDS) void pq_table_sub_kernel(PqTable p) {
+  static_assert(kDsub > 0 && kDsub <= 32, "sub-vectors held in registers");
+  __shared__ float subs[kTableQueries][kDsub];
+  const int s = static_cast<int>(blockIdx.y);
+  const int c = static_cast<int>(threadIdx.x);
+  const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kTableQueries;
+  const int nq = static_cast<int>(p.num_queries - q0 < kTableQueries ? p.num_queries - q0 : kTableQueries);
+  for (int i = c; i < nq * kDsub; i += VECTRA_PQ_CENTROIDS)
+    subs[i / kDsub][i % kDsub] = p.queries[(q0 + i / kDsub) * p.query_stride + static_cast<int64_t>(s) * kDsub + i % kDsub];
+  float centroid[kDsub];
+  const float* cp = p.codebooks + (static_cast<int64_t>(s) * VECTRA_PQ_CENTROIDS + c) * kDsub;
+#pragma unroll
+  for (int d = 0; d < kDsub; ++d) centroid[d] = cp[d];
+  __syncthreads();
+  for (int qq = 0; qq < nq; ++qq)
+    __builtin_nontemporal_store(table_entry<kDsub>(subs[qq], centroid, kDsub),
+                                &p.tables[(q0 + qq) * p.table_stride + static_cast<int64_t>(s) * VECTRA_PQ_CENTROIDS + c]);
 }
 
 struct PqAdc {
@@ -829,7 +869,18 @@ extern "C" int vectra_pq_distance_tables(const vectra_pq_table_args* a, hipStrea
   p.total = a->num_queries * entries;
   p.subspaces = a->subspaces;
   p.dsub = a->dimension / a->subspaces;
+  p.num_queries = static_cast<int32_t>(a->num_queries);
   void* args[] = {&p};
+  const void* sub_kernel = p.dsub == 8    ? reinterpret_cast<const void*>(&pq_table_sub_kernel<8>)
+                           : p.dsub == 4  ? reinterpret_cast<const void*>(&pq_table_sub_kernel<4>)
+                           : p.dsub == 16 ? reinterpret_cast<const void*>(&pq_table_sub_kernel<16>)
+                           : p.dsub == 32 ? reinterpret_cast<const void*>(&pq_table_sub_kernel<32>)
+                                          : nullptr;
+  if (sub_kernel != nullptr && p.subspaces <= kMaxBlocksY) {
+    const dim3 grid(static_cast<unsigned>((a->num_queries + kTableQueries - 1) / kTableQueries),
+                    static_cast<unsigned>(p.subspaces));
+    return launched(hipLaunchKernel(sub_kernel, grid, dim3(VECTRA_PQ_CENTROIDS), args, 0, stream));
+  }
   return launched(hipLaunchKernel(reinterpret_cast<const void*>(&pq_table_kernel), dim3(blocks_for(p.total, kThreads)),
                                   dim3(kThreads), args, 0, stream));
 }
