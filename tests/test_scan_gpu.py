@@ -82,12 +82,15 @@ def test_row_scans_against_the_oracle(dim, queries):
     _same(scan.squared_norms(_gpu(rows)), oracle.squared_norms(rows), 'norm')
 
 
-def test_strided_rows_and_queries_and_candidate_ids():
+# Several queries over 128-dimensional rows take the capped-grid kernel with
+# the queries in registers.
+@pytest.mark.parametrize('dim', [77, 128])
+def test_strided_rows_and_queries_and_candidate_ids(dim):
     rng = np.random.default_rng(5)
-    dim, n = 77, 2000
-    wide = torch.from_numpy(rng.standard_normal((n, 96)).astype(np.float32)).cuda()
-    rows = wide[:, 3:3 + dim]                  # row stride 96, offset 3 elements
-    qwide = torch.from_numpy(rng.standard_normal((6, 130)).astype(np.float32)).cuda()
+    n = 2000
+    wide = torch.from_numpy(rng.standard_normal((n, dim + 19)).astype(np.float32)).cuda()
+    rows = wide[:, 3:3 + dim]                  # row stride dim + 19, offset 3 elements
+    qwide = torch.from_numpy(rng.standard_normal((6, dim + 53)).astype(np.float32)).cuda()
     queries = qwide[:, 10:10 + dim]
     ids_np = rng.integers(0, n, 700).astype(np.int32)
     ids_np[[0, 5, 9]] = [n, n + 1000, 2**31 - 1]  # past the rows: NaN, and nothing read
@@ -109,16 +112,17 @@ def test_strided_rows_and_queries_and_candidate_ids():
     _same(out, want_ip, 'strided ip with uint32 ids')
 
 
-def test_special_values_propagate_like_the_reference():
-    dim = 40
+@pytest.mark.parametrize('dim,n_q', [(40, 1), (128, 5)])
+def test_special_values_propagate_like_the_reference(dim, n_q):
     rows = np.ones((6, dim), np.float32)
     rows[1, 3] = np.inf
     rows[2, 20] = np.nan
-    rows[3, 39] = -np.inf                       # in the tail
+    rows[3, 39] = -np.inf                       # in the tail at 40 dimensions
     rows[4, :] = 3e19                           # squares overflow to inf
     rows[5, :] = 1e-23                          # products underflow to subnormals and zero
-    q = np.zeros((1, dim), np.float32)
-    q[0, 3] = np.inf                            # inf - inf = NaN in row 1
+    q = np.zeros((n_q, dim), np.float32)
+    q[:, 3] = np.inf                            # inf - inf = NaN in row 1
+    q[1:, 7] = -2.5
     for fn, metric in ((scan.l2_squared_distances, 'l2'), (scan.inner_products, 'ip')):
         _same(fn(_gpu(q), _gpu(rows)), oracle.distances(q, rows, metric), metric)
     _same(scan.squared_norms(_gpu(rows)), oracle.squared_norms(rows), 'norm')
