@@ -90,7 +90,8 @@ def parse_args():
                    help='skip the plain-read ceiling measurement')
     p.add_argument('--scan', default=None,
                    help='benchmark a distance scan of the engine (vectra_amd/benchmarks/scan_workloads.py: '
-                   'flat_shard, flat_shard_q4, exhaustive, pq_shard, pq_tables) instead of the operator')
+                   'flat_shard, flat_shard_q4, exhaustive, pq_shard, pq_candidates, pq_tables, exhaustive_topk, '
+                   'single_topk) instead of the operator')
     return p.parse_args()
 
 
@@ -329,7 +330,10 @@ def _scan_cpu(w, inputs):
             return out_d, out_n
         return run, queries.shape[0] * n, ('reference' if lib is not None else 'port')
     if w.kind == 'adc':
-        codes = np.ascontiguousarray(inputs['codes'][:SCAN_CPU_ROWS].cpu().numpy())
+        if 'ids' in inputs:  # the codes the first candidates name, in candidate order
+            codes = np.ascontiguousarray(inputs['codes'][inputs['ids'][:SCAN_CPU_ROWS].long()].cpu().numpy())
+        else:
+            codes = np.ascontiguousarray(inputs['codes'][:SCAN_CPU_ROWS].cpu().numpy())
         tables = inputs['tables'].cpu().numpy()
         n = codes.shape[0]
 

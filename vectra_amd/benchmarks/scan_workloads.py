@@ -13,6 +13,9 @@ exhaustive    the exhaustive scan the reference actually runs: one query,
               2,048 rows (exhaustive_scan_threshold)
 pq_shard      PqAdcDistance of one query table over 4,000,000 16-byte codes
               (the ADC pass of a search over a whole shard)
+pq_candidates the same over 500,000 candidate ids drawn at random from the
+              shard's 4,000,000 codes (a candidate list's ADC pass: random
+              16-byte reads)
 pq_tables     ComputeDistanceTable for 1,024 queries (dimension 128,
               16 sub-spaces)
 exhaustive_   ShardIndex::ExhaustiveSearch for 1,024 queries at once, each
@@ -53,13 +56,15 @@ class Workload:
     subspaces: int = 16
     unit: str = 'distances/s'
     k: int = 0           # nearest rows kept per query ('topk')
+    ids: int = 0         # candidate ids drawn from the codes ('adc'; 0: every code)
 
     def algorithmic_bytes(self) -> int:
         if self.kind == 'rows':
             return self.count * self.dim * 4 + self.queries * self.dim * 4 + self.queries * self.count * 4
         if self.kind == 'adc':
-            return (self.count * self.subspaces + self.queries * self.subspaces * PQ_CENTROIDS * 4
-                    + self.queries * self.count * 4)
+            n = self.ids or self.count  # candidates: one code, (an id) and a distance each
+            return (n * self.subspaces + (4 * n if self.ids else 0)
+                    + self.queries * self.subspaces * PQ_CENTROIDS * 4 + self.queries * n * 4)
         if self.kind == 'topk':  # rows and queries in, k (distance, node) pairs out
             return self.count * self.dim * 4 + self.queries * self.dim * 4 + self.queries * self.k * 8
         # tables: queries + codebooks in, tables out
@@ -69,6 +74,8 @@ class Workload:
     def outputs_per_launch(self) -> int:
         if self.kind == 'tables':
             return self.queries * self.subspaces * PQ_CENTROIDS
+        if self.kind == 'adc' and self.ids:
+            return self.queries * self.ids
         return self.queries * self.count
 
     def set_bytes(self) -> int:
@@ -84,6 +91,7 @@ WORKLOADS = {w.name: w for w in (
     Workload('flat_shard_q4', 'rows', 4, 4_000_000),
     Workload('exhaustive', 'rows', 1, 2048),
     Workload('pq_shard', 'adc', 1, 4_000_000),
+    Workload('pq_candidates', 'adc', 1, 4_000_000, ids=500_000),
     Workload('pq_tables', 'tables', 1024, 0, unit='table entries/s'),
     Workload('exhaustive_topk', 'topk', 1024, 2048, k=10),
     Workload('single_topk', 'topk', 1, 2048, k=10),
@@ -122,6 +130,8 @@ def make_sets(w: Workload, seed: int = 0, device='cuda') -> list[dict]:
         for i in range(n_sets):
             sets.append({'tables': (torch.rand(w.queries, w.subspaces * PQ_CENTROIDS, generator=gen) * 8).to(device),
                          'codes': base if i == 0 else base ^ i})
+            if w.ids:
+                sets[-1]['ids'] = torch.randint(0, w.count, (w.ids,), generator=gen, dtype=torch.int32).to(device)
     else:
         for _ in range(n_sets):
             sets.append({'queries': torch.randn(w.queries, w.dim, generator=gen).to(device),
@@ -136,7 +146,7 @@ def make_output(w: Workload, device='cuda'):
                                                                         device=device))
     if w.kind == 'tables':
         return torch.empty(w.queries, w.subspaces * PQ_CENTROIDS, device=device)
-    return torch.empty(w.queries, w.count, device=device)
+    return torch.empty(w.queries, w.ids or w.count, device=device)
 
 
 def launch(w: Workload, inputs: dict, out: torch.Tensor) -> torch.Tensor:
@@ -146,5 +156,5 @@ def launch(w: Workload, inputs: dict, out: torch.Tensor) -> torch.Tensor:
     if w.kind == 'topk':
         return scan.nearest(inputs['queries'], inputs['rows'], w.k, out=out, workspace=inputs.get('workspace'))
     if w.kind == 'adc':
-        return scan.pq_adc_distances(inputs['tables'], inputs['codes'], out=out)
+        return scan.pq_adc_distances(inputs['tables'], inputs['codes'], ids=inputs.get('ids'), out=out)
     return scan.pq_distance_tables(inputs['queries'], inputs['codebooks'], w.subspaces, out=out)

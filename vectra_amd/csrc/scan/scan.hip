@@ -470,11 +470,40 @@ __global__ __launch_bounds__(kAdcThreads) void pq_adc_vec_kernel(PqAdc p) {
     const float d = valid ? adc_sum_words(chunk, m, entry) : NAN;
     if (at <= last) __builtin_nontemporal_store(d, &p.out[q * p.out_stride + at]);
   };
-  for (; cand <= last; cand += 2 * stride) {
-    load(cand + stride, valid_b, chunk_b);
-    emit(cand, valid_a, chunk_a);
-    load(cand + 2 * stride, valid_a, chunk_a);
-    emit(cand + stride, valid_b, chunk_b);
+  if constexpr (kIds) {
+    // A code's load waits for its id: the ids are requested a step ahead of
+    // their codes, in two more registers, so that the wait for step t + 1's
+    // id leaves step t's code in flight.  Issue order: id(t + 2), code(t + 1),
+    // id(t + 3), code(t + 2), ...; each wait is for the older of two loads.
+    uint32_t id_a = p.ids[cand + 2 * stride < last ? cand + 2 * stride : last];
+    uint32_t id_b = p.ids[cand + stride < last ? cand + stride : last];
+    auto code = [&](int64_t at, uint32_t id, bool& valid, uint4 (&chunk)[kChunks]) {
+      valid = at <= last && static_cast<int64_t>(id) < p.num_codes;
+      const int64_t index = valid ? static_cast<int64_t>(id) : 0;
+#pragma unroll
+      for (int k = 0; k < kChunks; ++k) {
+        const u32x4 x =
+            __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.codes + index * p.code_stride + 16 * k));
+        chunk[k] = make_uint4(x[0], x[1], x[2], x[3]);
+      }
+    };
+    for (; cand <= last; cand += 2 * stride) {
+      code(cand + stride, id_b, valid_b, chunk_b);
+      const int64_t n3 = cand + 3 * stride;
+      id_b = p.ids[n3 < last ? n3 : last];
+      emit(cand, valid_a, chunk_a);
+      code(cand + 2 * stride, id_a, valid_a, chunk_a);
+      const int64_t n4 = cand + 4 * stride;
+      id_a = p.ids[n4 < last ? n4 : last];
+      emit(cand + stride, valid_b, chunk_b);
+    }
+  } else {
+    for (; cand <= last; cand += 2 * stride) {
+      load(cand + stride, valid_b, chunk_b);
+      emit(cand, valid_a, chunk_a);
+      load(cand + 2 * stride, valid_a, chunk_a);
+      emit(cand + stride, valid_b, chunk_b);
+    }
   }
 }
 
