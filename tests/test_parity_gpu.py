@@ -119,6 +119,23 @@ def test_long_key_rows_against_the_expansion():
             np.testing.assert_allclose(got, want, **HALF_TOL)
 
 
+@pytest.mark.parametrize('n_q', [1, 17, 255, 257, 300])
+@pytest.mark.parametrize('dim', [32, 64])
+def test_long_keys_with_partial_work_items(n_q, dim):
+    # Query counts around the tile kernel's work items (128 rows for 32-dim
+    # heads, 256 for 64-dim), on a key axis long enough for its fp16-weight
+    # pass: the default output, both head-dim kernels, against the expansion.
+    gen = torch.Generator().manual_seed(n_q * 3 + dim)
+    q = (0.5 * torch.randn(1, 2, n_q, dim, generator=gen)).bfloat16()
+    k = (0.5 * torch.randn(1, 2, 1100, dim, generator=gen)).bfloat16()
+    v = (0.25 * torch.randn(1, 2, 1100, dim, generator=gen)).bfloat16()
+    scale = torch.tensor([0.02, 0.04]).reshape(1, 2, 1, 1)
+    want = oracle.expanded_fp64(q, k, v, scale)
+    print(f'long keys n_q={n_q} dim={dim}', flush=True)
+    got = run(q, k, v, scale, None, 'tile').double().numpy()
+    np.testing.assert_allclose(got, want, **HALF_TOL)
+
+
 def test_operator_output_is_the_rounded_fp32_result():
     inputs = configs.make_inputs(configs.SERVING, seed=1).to('cuda')
     out = torch.ops.vectra.rbf_attention(*inputs.args())
