@@ -300,12 +300,15 @@ def test_nearest_equals_the_reference_outputs(golden):
         assert (got_n.cpu().numpy()[0, m:] == scan.NO_NODE).all() and torch.isinf(got_d[0, m:]).all()
 
 
-# Up to 1023 queries take 16-wave workgroups, from 1024 on 4-wave ones.
+# Up to 1023 queries take 16-wave workgroups, from 1024 on 4-wave ones; k up
+# to 64 / waves takes the wave-sort first selection (4 and 16 here), 17 the
+# LDS sort.
 @pytest.mark.parametrize('n,dim,k,queries', [(2048, 128, 10, 4), (2048, 128, 100, 2), (700, 17, 1, 3),
                                              (5000, 32, 1024, 2), (300, 300, 64, 2), (100, 0, 20, 2),
                                              (1, 8, 5, 1), (30, 16, 1024, 1), (300, 24, 16, 1100),
                                              (2048, 128, 10, 1024), (5000, 128, 1024, 2), (2999, 128, 7, 1030),
-                                             (3001, 128, 64, 3)])
+                                             (3001, 128, 64, 3), (3001, 128, 4, 5), (2048, 128, 16, 1024),
+                                             (2048, 128, 17, 1024)])
 def test_nearest_against_the_oracle(n, dim, k, queries):
     rng = np.random.default_rng(n + dim + k)
     rows = rng.standard_normal((n, dim)).astype(np.float32)

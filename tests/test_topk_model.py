@@ -26,7 +26,7 @@ def _case(rng, n, k, skip_frac, descending=False, dup_frac=0.0):
 
 
 @pytest.mark.parametrize('form', ['split', 'narrow', 'wide', 'wide128'])
-@pytest.mark.parametrize('k', [1, 10, 64, 65, 500, 993, 1000, 1024])
+@pytest.mark.parametrize('k', [1, 4, 5, 10, 16, 17, 54, 64, 65, 500, 993, 1000, 1024])
 def test_the_selection_keeps_the_k_smallest(form, k):
     rng = np.random.default_rng(k * 7 + len(form))
     for n, skip, desc in ((k // 2 + 1, 0.0, False), (k + 37, 0.03, False), (2 * k + 130, 0.02, False),

@@ -13,6 +13,8 @@ CPU against a plain sort of the candidates:
     round loop      scan.hip scan_top_k_kernel, the `for (base ...)` loop
     merge trigger   `(worst == kNoKey && n >= k) || n > kTopKKeys - k - round`
     first_select    one wave sorts the <= 64 new keys into keys[0 .. 64)
+    wave_select     one wave sorts keys[0 .. k + n) (k + n <= 64), or each
+                    wave the k best of its 64 candidates, then one wave those
     merge           bitonic sort of keys[0 .. k + n), padded to a power of 2
     split merge     k-way merge of the ranges' sorted lists (k, splits <= 64)
                     or a full sort of them
@@ -49,14 +51,37 @@ def round_len(form):
     return threads // 16 * cands * steps
 
 
-def _select(keys, k, n, first, rnd):
-    """select(first, n): first_select when a round fits one wave, else merge."""
+def _select(keys, k, n, first, rnd, threads):
+    """select(first, n): first_select when a round fits one wave; else, in
+    kernels whose rounds exceed a wave, the wave sorts (wave_select: k + n <=
+    64 in one wave, or a first selection of at most one candidate per thread
+    with k <= 64 / waves, each wave keeping the k best of its 64 and one wave
+    sorting those lists); else merge."""
     if rnd <= WAVE and first and n <= WAVE:
         lanes = np.full(WAVE, NO_KEY, dtype=np.uint64)
         lanes[:n] = keys[k:k + n]
         lanes.sort()
         m = min(k, WAVE)
         keys[:m] = lanes[:m]
+        return
+    waves = threads // WAVE
+    if rnd <= WAVE:
+        pass  # the split form's kernel has no wave_select
+    elif k + n <= WAVE:
+        lanes = np.full(WAVE, NO_KEY, dtype=np.uint64)
+        lanes[:k + n] = keys[:k + n]
+        lanes.sort()
+        keys[:k] = lanes[:k]
+        return
+    elif first and n <= threads and waves * k <= WAVE:
+        lanes = np.full(threads, NO_KEY, dtype=np.uint64)
+        lanes[:n] = keys[k:k + n]
+        per_wave = np.sort(lanes.reshape(waves, WAVE), axis=1)[:, :k]
+        keys[:waves * k] = per_wave.reshape(-1)
+        best = np.full(WAVE, NO_KEY, dtype=np.uint64)
+        best[:waves * k] = keys[:waves * k]
+        best.sort()
+        keys[:k] = best[:k]
         return
     size = 2
     while size < k + n:
@@ -85,13 +110,13 @@ def range_k_best(cand_keys, k, form, empty_test='merged'):
         n = fill
         if (worst == NO_KEY and n >= k) or n > KEYS - k - rnd:
             first = (not merged) if empty_test == 'merged' else (worst == NO_KEY)
-            _select(keys, k, n, first, rnd)
+            _select(keys, k, n, first, rnd, FORMS[form][0])
             merged = True
             fill = 0
             worst = keys[k - 1]
     if fill > 0:
         first = (not merged) if empty_test == 'merged' else (worst == NO_KEY)
-        _select(keys, k, fill, first, rnd)
+        _select(keys, k, fill, first, rnd, FORMS[form][0])
     return keys[:k].copy()
 
 
