@@ -766,6 +766,11 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
   };
 
   uint64_t worst = kNoKey;  // the k-th best key so far; empty while fewer than k
+  // Its distance (NaN while empty): a candidate whose distance is above it
+  // cannot beat it, and its key is not formed.  NaN distances, and every
+  // candidate while `worst` is empty, fail `sum > worst_d` and go on to the
+  // key comparison, so the filter drops only candidates the keys would.
+  float worst_d = key_distance(kNoKey);
   // Whether keys[0 .. k) hold a selection.  An overflow merge can keep fewer
   // than k keys (ids past the rows are skipped), which leaves `worst` empty
   // with keys in the buffer, so `worst` cannot tell an empty buffer.
@@ -780,6 +785,7 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
       selected = true;
       if (tid == 0) fill = 0;
       worst = keys[k - 1];
+      worst_d = key_distance(worst);
       __syncthreads();
     }
   };
@@ -829,7 +835,7 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
 #pragma unroll
         for (int u = 0; u < kPer; ++u) sum = sum + term<VECTRA_SCAN_L2_SQUARED>(qv[u], st.v[c][u]);
         sum = reduce_lanes(sum);
-        if (st.ok[c] && lane == 0) {
+        if (st.ok[c] && lane == 0 && !(sum > worst_d)) {
           const uint64_t key = nearest_key(sum, st.row[c]);
           if (key < worst) keys[k + atomicAdd(&fill, 1u)] = key;
         }
@@ -897,7 +903,7 @@ __global__ __launch_bounds__(kTopKThreads) void scan_top_k_kernel(TopK p) {
           float t = 0.f;
           if (valid[c] && lane < tail) t = term<VECTRA_SCAN_L2_SQUARED>(qlane[full], rlane[c][full]);
           for (int e = 0; e < tail; ++e) sum = sum + __shfl(t, e, kLanes);
-          if (valid[c] && lane == 0) {
+          if (valid[c] && lane == 0 && !(sum > worst_d)) {
             const uint64_t key = nearest_key(sum, static_cast<uint32_t>(row[c]));
             if (key < worst) keys[k + atomicAdd(&fill, 1u)] = key;
           }
