@@ -617,32 +617,84 @@ __device__ __forceinline__ float key_distance(uint64_t key) {
   return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
 }
 
-// Wave-wide operations on one 64-bit key per lane (lane shuffles: no LDS
-// buffer and no barrier).
+// Wave-wide operations on one 64-bit key per lane, with no LDS buffer and
+// no barrier: the partner exchanges are DPP moves and permlane swaps, which
+// stay in the vector unit (an LDS permute, ds_bpermute, is a round trip
+// through the LDS pipeline for every 32-bit half of every stage).
 constexpr int kWaveLanes = 64;
 
-// Bitonic sort across the wave: lane i ends with the i-th smallest key.
-__device__ __forceinline__ uint64_t wave_sort(uint64_t key, int lane) {
-#pragma unroll
-  for (int size = 2; size <= kWaveLanes; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const uint64_t other = __shfl_xor(key, stride, kWaveLanes);
-      const bool keep_min = ((lane & stride) == 0) == ((lane & size) == 0);
-      const uint64_t lo = key < other ? key : other, hi = key < other ? other : key;
-      key = keep_min ? lo : hi;
-    }
+// The value of lane `lane ^ kStride` (kStride a power of two below 64).
+template <int kStride>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t x, int lane) {
+  static_assert(kStride >= 1 && kStride <= 32 && (kStride & (kStride - 1)) == 0, "a lane bit");
+  if constexpr (kStride == 1) {
+    return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false);  // quad_perm [1, 0, 3, 2]
+  } else if constexpr (kStride == 2) {
+    return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (kStride == 4 || kStride == 8) {
+    // Within a row of 16: row_shl:s gives lane i lane i + s, row_shr:s lane i - s.
+    const uint32_t up = __builtin_amdgcn_mov_dpp(x, 0x100 + kStride, 0xf, 0xf, false);
+    const uint32_t down = __builtin_amdgcn_mov_dpp(x, 0x110 + kStride, 0xf, 0xf, false);
+    return (lane & kStride) ? down : up;
+  } else if constexpr (kStride == 16) {
+    // v_permlane16_swap(x, x): the first result holds rows 0, 0, 2, 2 of x,
+    // the second rows 1, 1, 3, 3.
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    // v_permlane32_swap(x, x): the first result holds x's low half twice,
+    // the second its high half twice.
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (lane & 32) ? r[0] : r[1];
   }
-  return key;
+}
+template <int kStride>
+__device__ __forceinline__ uint64_t lane_xor(uint64_t key, int lane) {
+  const uint32_t lo = lane_xor<kStride>(static_cast<uint32_t>(key), lane);
+  const uint32_t hi = lane_xor<kStride>(static_cast<uint32_t>(key >> 32), lane);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-// The smallest key of the wave, in every lane.
+// One compare-exchange stage of the bitonic network.
+template <int kSize, int kStride>
+__device__ __forceinline__ uint64_t bitonic_stage(uint64_t key, int lane) {
+  const uint64_t other = lane_xor<kStride>(key, lane);
+  const bool keep_min = ((lane & kStride) == 0) == ((lane & kSize) == 0);
+  const uint64_t lo = key < other ? key : other, hi = key < other ? other : key;
+  return keep_min ? lo : hi;
+}
+template <int kSize, int kStride>
+__device__ __forceinline__ uint64_t bitonic_merge(uint64_t key, int lane) {
+  key = bitonic_stage<kSize, kStride>(key, lane);
+  if constexpr (kStride > 1) key = bitonic_merge<kSize, kStride / 2>(key, lane);
+  return key;
+}
+template <int kSize>
+__device__ __forceinline__ uint64_t bitonic_sort(uint64_t key, int lane) {
+  if constexpr (kSize > 2) key = bitonic_sort<kSize / 2>(key, lane);
+  return bitonic_merge<kSize, kSize / 2>(key, lane);
+}
+
+// Bitonic sort across the wave: lane i ends with the i-th smallest key (one
+// query over 2,048 rows, the split form: 11.3 -> 9.5 us against the same
+// network on LDS permutes; 1,024 queries: unchanged, 59.2-59.7 us both).
+__device__ __forceinline__ uint64_t wave_sort(uint64_t key, int lane) {
+  return bitonic_sort<kWaveLanes>(key, lane);
+}
+
+// The smallest key of the wave, in every lane (the split form's merge).
 __device__ __forceinline__ uint64_t wave_min(uint64_t key) {
-#pragma unroll
-  for (int mask = kWaveLanes / 2; mask > 0; mask >>= 1) {
-    const uint64_t other = __shfl_xor(key, mask, kWaveLanes);
+  const int lane = static_cast<int>(threadIdx.x) & (kWaveLanes - 1);
+  auto step = [&](auto s_tag) {
+    const uint64_t other = lane_xor<decltype(s_tag)::value>(key, lane);
     key = other < key ? other : key;
-  }
+  };
+  step(std::integral_constant<int, 32>{});
+  step(std::integral_constant<int, 16>{});
+  step(std::integral_constant<int, 8>{});
+  step(std::integral_constant<int, 4>{});
+  step(std::integral_constant<int, 2>{});
+  step(std::integral_constant<int, 1>{});
   return key;
 }
 
