@@ -65,7 +65,10 @@ typedef enum vectra_scan_metric {
 /*
  * Row scan: out[q * out_stride + i] = metric(query q, row ids[i]) for every
  * query q < num_queries and candidate i < num_ids, or of row i for
- * i < num_rows when ids is NULL.  Query q is `dimension` floats at
+ * i < num_rows when ids is NULL.  (In every entry point here a NULL `ids`
+ * means every row whatever num_ids is; an empty candidate list is a
+ * non-NULL `ids` with num_ids 0, of which nothing is read.  A zero-size
+ * allocation may come back NULL: pass any valid pointer for it.)  Query q is `dimension` floats at
  * queries + q * query_stride; row r at rows + r * row_stride.  For
  * VECTRA_SCAN_SQUARED_NORM, `queries` is unused and num_queries must be 1.
  * With dimension 0 every output is 0 and `queries` and `rows` may be NULL.

@@ -428,3 +428,35 @@ def test_nearest_matches_the_row_scan_and_a_sort():
     order = torch.from_numpy(np.argsort(full.cpu().numpy(), axis=1, kind='stable')[:, :50])
     assert torch.equal(nodes.cpu().to(torch.int64), order)
     _same(d, torch.gather(full.cpu(), 1, order))
+
+
+@pytest.mark.parametrize('form', scan.TOP_K_FORMS)
+def test_an_empty_candidate_list_selects_nothing(form):
+    """An empty ids tensor (whose data pointer is NULL) means no candidates, not
+    every row: the NULL `ids` of the C ABI is reserved for "every row"."""
+    g = torch.Generator().manual_seed(7)
+    rows = torch.randn(300, 32, generator=g).cuda()
+    queries = torch.randn(3, 32, generator=g).cuda()
+    empty = torch.zeros(0, dtype=torch.int32, device='cuda')
+    d, n = scan.nearest(queries, rows, 10, empty, form=form)
+    torch.cuda.synchronize()
+    assert torch.isinf(d).all() and bool((d > 0).all())
+    assert bool((n.cpu().to(torch.int64) == scan.NO_NODE).all())
+    want_d, want_n = oracle.nearest(queries.cpu().numpy(), rows.cpu().numpy(), 10, np.zeros(0, dtype=np.int64))
+    assert np.array_equal(d.cpu().numpy(), want_d) and np.array_equal(n.cpu().numpy(), want_n)
+
+
+def test_an_empty_candidate_list_scans_nothing():
+    g = torch.Generator().manual_seed(8)
+    rows = torch.randn(50, 16, generator=g).cuda()
+    queries = torch.randn(2, 16, generator=g).cuda()
+    empty = torch.zeros(0, dtype=torch.int32, device='cuda')
+    for fn in (scan.l2_squared_distances, scan.inner_products):
+        out = fn(queries, rows, empty)
+        torch.cuda.synchronize()
+        assert tuple(out.shape) == (2, 0)
+    codes = torch.randint(0, 256, (40, 4), dtype=torch.uint8, generator=g).cuda()
+    tables = torch.randn(2, 4 * 256, generator=g).cuda()
+    out = scan.pq_adc_distances(tables, codes, empty)
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (2, 0)

@@ -127,6 +127,24 @@ def _ids(ids, like: torch.Tensor):
     return ids.contiguous()
 
 
+# A NULL `ids` means every row to the C ABI, and the data pointer of an empty
+# tensor is NULL: an empty candidate list is passed as this one-element
+# buffer with a count of 0 (the library reads none of it).
+_EMPTY_IDS = {}
+
+
+def _ids_ptr(ids):
+    """The C ABI's `ids` for a candidate tensor (None: every row)."""
+    if ids is None:
+        return None
+    if ids.numel() > 0:
+        return ids.data_ptr()
+    dev = ids.device
+    if dev not in _EMPTY_IDS:
+        _EMPTY_IDS[dev] = torch.zeros(1, dtype=torch.int32, device=dev)
+    return _EMPTY_IDS[dev].data_ptr()
+
+
 def _out(out, shape, device) -> torch.Tensor:
     if out is None:
         return torch.empty(shape, dtype=torch.float32, device=device)
@@ -158,7 +176,7 @@ def _scan_rows(metric, queries, rows, ids, out):
     count = rows.shape[0] if ids is None else ids.shape[0]
     out = _out(out, (num_queries, count), rows.device)
     args = _ScanArgs(metric, dim, q_ptr, num_queries, q_stride, rows.data_ptr(), rows.shape[0], _row_stride(rows),
-                     None if ids is None else ids.data_ptr(), 0 if ids is None else ids.shape[0],
+                     _ids_ptr(ids), 0 if ids is None else ids.shape[0],
                      out.data_ptr(), out.stride(0) if num_queries > 1 else max(count, 1))
     with torch.cuda.device(rows.device):
         _check(_native.scan_library().vectra_scan_rows(ctypes.byref(args), _stream(rows.device)))
@@ -213,7 +231,7 @@ def pq_adc_distances(tables: torch.Tensor, codes: torch.Tensor, ids=None, out=No
     out = _out(out, (tables.shape[0], count), codes.device)
     args = _PqAdcArgs(subspaces, tables.data_ptr(), tables.shape[0], _row_stride(tables),
                       codes.data_ptr(), codes.shape[0], _row_stride(codes),
-                      None if ids is None else ids.data_ptr(), 0 if ids is None else ids.shape[0],
+                      _ids_ptr(ids), 0 if ids is None else ids.shape[0],
                       out.data_ptr(), out.stride(0) if tables.shape[0] > 1 else max(count, 1))
     with torch.cuda.device(codes.device):
         _check(_native.scan_library().vectra_scan_pq_adc(ctypes.byref(args), _stream(codes.device)))
@@ -240,7 +258,7 @@ def _top_k_args(queries, rows, k, ids, out):
                 raise ValueError(f'out must be contiguous ({n_q}, {k}) float32 and uint32 tensors')
     args = _TopKArgs(rows.shape[1], k, queries.data_ptr(), n_q, _row_stride(queries),
                      rows.data_ptr(), rows.shape[0], _row_stride(rows),
-                     None if ids is None else ids.data_ptr(), 0 if ids is None else ids.shape[0],
+                     _ids_ptr(ids), 0 if ids is None else ids.shape[0],
                      distances.data_ptr(), nodes.data_ptr(), k)
     # The tensors the arguments point into stay referenced with them.
     return args, (queries, rows, ids), distances, nodes
