@@ -103,6 +103,26 @@ def test_variant_selection(kwargs, variant):
     assert capi.VARIANT_NAMES[capi.select_variant(_fake_args(**kwargs))] == variant
 
 
+def test_negative_key_row_strides_go_to_the_generic_kernel():
+    """The stream, plane, tile and MFMA kernels address key rows through
+    unsigned 32-bit offsets within a plane; K, V or bias rows walked
+    backwards (negative strides, which the ABI accepts) take the kernel with
+    64-bit signed addressing."""
+    for n in (64, 65, 100):
+        assert capi.VARIANT_NAMES[capi.select_variant(_fake_args(n_q=n if n > 64 else 1, n_k=n))] != 'generic'
+        for name, dim in (('k_stride', 32), ('v_stride', 32)):
+            a = _fake_args(n_q=n if n > 64 else 1, n_k=n)
+            setattr(a, name, (ctypes.c_int64 * 4)(8 * n * dim, n * dim, -dim, 1))
+            assert capi.VARIANT_NAMES[capi.select_variant(a)] == 'generic', (n, name)
+        a = _fake_args(n_q=n if n > 64 else 1, n_k=n)
+        a.key_bias, a.bias_stride_b, a.bias_stride_h, a.bias_stride_n = (1 << 20) + (5 << 16), n, 0, -1
+        assert capi.VARIANT_NAMES[capi.select_variant(a)] == 'generic', (n, 'bias')
+        for variant in ('stream', 'plane', 'tile', 'mfma'):
+            a = _fake_args(n_q=n if n > 64 else 1, n_k=n, variant=variant)
+            a.k_stride = (ctypes.c_int64 * 4)(8 * n * 32, n * 32, -32, 1)
+            assert capi.select_variant(a) == -capi.ERR_BAD_VARIANT, (n, variant)
+
+
 def test_plane_kernel_needs_disjoint_rows_within_32_bit_offsets():
     """The plane kernel reads K and V through buffer extents that end at the
     last row, so rows past Nk read as zeros only when rows do not overlap; and

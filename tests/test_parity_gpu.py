@@ -463,6 +463,32 @@ def test_empty_key_set_gives_zeros():
         assert torch.equal(run(q, k, v, torch.tensor(0.1), None, variant), torch.zeros(1, 2, 3, 32))
 
 
+@pytest.mark.parametrize('n_q,n_k', [(1, 64), (65, 65), (100, 100)])
+def test_key_rows_walked_backwards(n_q, n_k):
+    """Negative key-row strides (K, V and the bias addressed from their last
+    key row), which the ABI accepts: the result is that of the reversed keys,
+    from the kernel with signed 64-bit addressing (the shapes are the stream,
+    plane and tile kernels' with forward strides)."""
+    gen = torch.Generator().manual_seed(21 + n_k)
+    q = torch.randn(2, 4, n_q, 32, generator=gen).to(torch.bfloat16)
+    k = torch.randn(2, 4, n_k, 32, generator=gen).to(torch.bfloat16)
+    v = torch.randn(2, 4, n_k, 32, generator=gen).to(torch.bfloat16)
+    bias = torch.randn(2, 1, 1, n_k, generator=gen)
+    scale = torch.tensor(0.05)
+    want = oracle.direct_fp64(q, k.flip(2), v.flip(2), scale, bias.flip(3))
+    qd, kd, vd, sd, bd = (x.cuda() for x in (q, k, v, scale, bias))
+    scale4, bias4 = capi.broadcast_operands(qd, kd, sd, bd)
+    out = torch.full((2, 4, n_q, 32), float('nan'), device='cuda')
+    a = capi.make_args(qd, kd, vd, out, scale4, bias4)
+    a.k, a.v = kd[:, :, n_k - 1].data_ptr(), vd[:, :, n_k - 1].data_ptr()
+    a.k_stride[2], a.v_stride[2] = -kd.stride(2), -vd.stride(2)
+    a.key_bias, a.bias_stride_n = bias4[:, :, :, n_k - 1].data_ptr(), -bias4.stride(3)
+    assert capi.VARIANT_NAMES[capi.select_variant(a)] == 'generic'
+    capi.launch(a)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out.cpu().double().numpy(), want, **HALF_TOL)
+
+
 def test_operator_with_a_cpu_scalar_scale_and_outputs_in_every_dtype():
     gen = torch.Generator().manual_seed(10)
     q, k, v = (torch.randn(2, 3, n, 32, generator=gen) for n in (4, 50, 50))

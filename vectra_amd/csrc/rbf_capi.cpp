@@ -159,7 +159,10 @@ int stream_chunks(const vectra_rbf_args* a) {
   // 8- and 16-chunk rows run one key tile per row only (more would spill
   // registers in the looping variant).
   if (chunks >= 8 && a->n_k > 64) return 0;
-  // Per-lane key offsets inside a (b, h) plane are 32-bit.
+  // Per-lane key offsets inside a (b, h) plane are unsigned 32-bit: key row
+  // strides (K, V and the bias) must be non-negative and the last row's
+  // bytes within 2^31.
+  if (a->k_stride[2] < 0 || a->v_stride[2] < 0 || (a->key_bias != nullptr && a->bias_stride_n < 0)) return 0;
   const int64_t limit = int64_t{1} << 31;
   const int64_t last_key = a->n_k > 0 ? a->n_k - 1 : 0;
   if (last_key * a->k_stride[2] * in_sz + 16 * chunks >= limit ||
