@@ -76,7 +76,8 @@ enum {
 /*
  * Problem description.  All strides are in ELEMENTS of the tensor they
  * describe and may be zero (broadcast) or arbitrary (head-transposed views,
- * spatial_rbf_attention.py:31-32).
+ * spatial_rbf_attention.py:31-32; negative ones too, which the generic
+ * kernel serves: the faster kernels address rows by unsigned offsets).
  *
  *   q   [B, H, Nq, D]    k [B, H, Nk, D]    v [B, H, Nk, Dv]
  *   out [B, H, Nq, Dv]   written in out_dtype (the operator passes v.dtype;
