@@ -308,7 +308,7 @@ def test_nearest_equals_the_reference_outputs(golden):
                                              (1, 8, 5, 1), (30, 16, 1024, 1), (300, 24, 16, 1100),
                                              (2048, 128, 10, 1024), (5000, 128, 1024, 2), (2999, 128, 7, 1030),
                                              (3001, 128, 64, 3), (3001, 128, 4, 5), (2048, 128, 16, 1024),
-                                             (2048, 128, 17, 1024)])
+                                             (2048, 128, 17, 1024), (2050, 128, 33, 1031), (3000, 128, 1024, 1025)])
 def test_nearest_against_the_oracle(n, dim, k, queries):
     rng = np.random.default_rng(n + dim + k)
     rows = rng.standard_normal((n, dim)).astype(np.float32)
@@ -316,6 +316,26 @@ def test_nearest_against_the_oracle(n, dim, k, queries):
     q = rng.standard_normal((queries, dim)).astype(np.float32)
     print(f'nearest n={n} dim={dim} k={k} queries={queries}', flush=True)
     _check_nearest(q, rows, k, msg=f'n={n} dim={dim} k={k}')
+
+
+def test_nearest_for_many_queries_with_candidate_ids():
+    """From 1024 queries up (4-wave workgroups, 128-dimensional rows in the
+    pipelined kernel): an odd query count, two equal queries, candidate ids
+    with duplicates, ids past the row count and NaN and infinite distances,
+    k from 1 to 1024 (overflow merges)."""
+    rng = np.random.default_rng(41)
+    n = 1500
+    rows = rng.standard_normal((n, 128)).astype(np.float32)
+    rows[5, 3] = np.nan
+    rows[6, 0] = np.inf
+    q = rng.standard_normal((1027, 128)).astype(np.float32)
+    q[1] = q[0]  # equal keys for two queries
+    ids = rng.integers(0, n + 300, 2400).astype(np.uint32)
+    ids[:100] = ids[100:200]
+    ids[200:202] = [5, 6]
+    for k in (1, 10, 1000, 1024):
+        print(f'nearest ids queries=1027 k={k}', flush=True)
+        _check_nearest(q, rows, k, ids=ids, msg=f'k={k}')
 
 
 # 128-dimensional rows take the pipelined kernels (two register sets of rows).
