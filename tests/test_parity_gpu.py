@@ -463,6 +463,19 @@ def test_empty_key_set_gives_zeros():
         assert torch.equal(run(q, k, v, torch.tensor(0.1), None, variant), torch.zeros(1, 2, 3, 32))
 
 
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize('n_q,n_k', [(81, 65), (127, 65), (127, 80), (200, 80), (80, 65), (127, 64), (127, 81)])
+def test_mfma_variant_64_dim_heads_around_80_keys(dtype, n_q, n_k):
+    """The MFMA kernel at 64-dim 16-bit heads, key axes of 64 to 81 and query
+    counts on both sides of five 16-row tiles (where the launch changes its
+    wave count and key tile), every output against the float64 chain."""
+    gen = torch.Generator().manual_seed(n_q * 1000 + n_k)
+    q, k, v = (torch.randn(2, 4, n, 64, generator=gen).to(dtype) for n in (n_q, n_k, n_k))
+    scale = torch.tensor(0.5 / 64)
+    want = oracle.direct_fp64(q, k, v, scale)
+    np.testing.assert_allclose(run(q, k, v, scale, variant='mfma').double().numpy(), want, **HALF_TOL)
+
+
 @pytest.mark.parametrize('n_q,n_k', [(1, 64), (65, 65), (100, 100)])
 def test_key_rows_walked_backwards(n_q, n_k):
     """Negative key-row strides (K, V and the bias addressed from their last

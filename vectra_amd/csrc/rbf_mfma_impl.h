@@ -542,7 +542,12 @@ hipError_t launch_mfma_d(Problem& p, hipStream_t s) {
     if (p.Nk <= 32) return launch_mfma_k<T, OutT, kD, 32>(p, s);
     if constexpr (kMax >= 128) {
       if (p.Nk <= 64) return launch_mfma_k<T, OutT, kD, 64>(p, s);
-      if (p.Nk <= 80) return launch_mfma_k<T, OutT, kD, 80>(p, s);
+      // 16-bit 64-dim heads with more than five query tiles (eight waves)
+      // take the 128-key tile instead of the 80-key one: that instantiation
+      // returned wrong values in value dims 32-63 on the device (cause not
+      // found; every other instantiation matched the oracle).
+      const bool avoid80 = sizeof(T) == 2 && kD == 64 && (p.Nq + 15) / 16 > 5;
+      if (p.Nk <= 80 && !avoid80) return launch_mfma_k<T, OutT, kD, 80>(p, s);
       return launch_mfma_k<T, OutT, kD, 128>(p, s);
     } else {
       return launch_mfma_k<T, OutT, kD, 64>(p, s);
