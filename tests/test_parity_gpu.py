@@ -463,6 +463,28 @@ def test_empty_key_set_gives_zeros():
         assert torch.equal(run(q, k, v, torch.tensor(0.1), None, variant), torch.zeros(1, 2, 3, 32))
 
 
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16, torch.float32], ids=str)
+@pytest.mark.parametrize('dim', [16, 32, 64, 128])
+def test_every_variant_over_a_grid_of_shapes(dtype, dim):
+    """Every variant that accepts the shape, over key and query counts on
+    both sides of the kernels' tile, slot and wave-count boundaries (1, 16,
+    17, 64, 65, 80, 81, 129 keys; 1, 16, 65, 81, 127 queries), against the
+    float64 chain at the dtype's gate."""
+    gen = torch.Generator().manual_seed(dim)
+    tol = FP32_TOL if dtype == torch.float32 else HALF_TOL
+    for n_k in (1, 16, 17, 64, 65, 80, 81, 129):
+        for n_q in (1, 16, 65, 81, 127):
+            q = (0.5 * torch.randn(2, 3, n_q, dim, generator=gen)).to(dtype)
+            k = (0.5 * torch.randn(2, 3, n_k, dim, generator=gen)).to(dtype)
+            v = torch.randn(2, 3, n_k, dim, generator=gen).to(dtype)
+            scale = torch.tensor(0.5 / dim)
+            want = oracle.direct_fp64(q, k, v, scale)
+            for variant in _variants(q, k, v, scale, None):
+                print(f'grid dtype={dtype} dim={dim} n_k={n_k} n_q={n_q} variant={variant}', flush=True)
+                got = run(q, k, v, scale, None, variant).double().numpy()
+                np.testing.assert_allclose(got, want, err_msg=f'{variant} n_k={n_k} n_q={n_q}', **tol)
+
+
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize('n_q,n_k', [(81, 65), (127, 65), (127, 80), (200, 80), (80, 65), (127, 64), (127, 81)])
 def test_mfma_variant_64_dim_heads_around_80_keys(dtype, n_q, n_k):
