@@ -237,13 +237,16 @@ __global__ __launch_bounds__(64 * kWaves) void rbf_mfma_kernel(Problem p, int32_
 #pragma unroll
     for (int s = 0; s < Stage::kKSlots; ++s) {
       const int slot = tid + s * kThreads;
-      if (Stage::kKSlots * kThreads == kKeys * kDChunks || slot < kKeys * kDChunks) {
-        const int key = slot / kDChunks;
-        const uint4 raw = j0 + key < n_k ? st.k[s] : make_uint4(0, 0, 0, 0);
-        *reinterpret_cast<uint4*>(k_lds + key * Geo::kKStride + (slot % kDChunks) * kVec) = raw;
-        const float sq = reduce_low<kDChunks>(dot_chunk<T>(raw, raw, 0.f), OpSum());
-        if (slot % kDChunks == 0) kn_lds[key] = -0.5f * sq;
-      }
+      // The cross-lane reduction runs on every lane, outside any branch, and
+      // only the stores are guarded: under a branch that some waves skip (a
+      // slot only partly filled, as with eight waves and 80-key tiles of
+      // 64-dim rows) its DPP reads gave wrong values on the device.
+      const bool live = Stage::kKSlots * kThreads == kKeys * kDChunks || slot < kKeys * kDChunks;
+      const int key = slot / kDChunks;
+      const uint4 raw = live && j0 + key < n_k ? st.k[s] : make_uint4(0, 0, 0, 0);
+      if (live) *reinterpret_cast<uint4*>(k_lds + key * Geo::kKStride + (slot % kDChunks) * kVec) = raw;
+      const float sq = reduce_low<kDChunks>(dot_chunk<T>(raw, raw, 0.f), OpSum());
+      if (live && slot % kDChunks == 0) kn_lds[key] = -0.5f * sq;
     }
 #pragma unroll
     for (int s = 0; s < Stage::kVSlots; ++s) {
@@ -542,12 +545,7 @@ hipError_t launch_mfma_d(Problem& p, hipStream_t s) {
     if (p.Nk <= 32) return launch_mfma_k<T, OutT, kD, 32>(p, s);
     if constexpr (kMax >= 128) {
       if (p.Nk <= 64) return launch_mfma_k<T, OutT, kD, 64>(p, s);
-      // 16-bit 64-dim heads with more than five query tiles (eight waves)
-      // take the 128-key tile instead of the 80-key one: that instantiation
-      // returned wrong values in value dims 32-63 on the device (cause not
-      // found; every other instantiation matched the oracle).
-      const bool avoid80 = sizeof(T) == 2 && kD == 64 && (p.Nq + 15) / 16 > 5;
-      if (p.Nk <= 80 && !avoid80) return launch_mfma_k<T, OutT, kD, 80>(p, s);
+      if (p.Nk <= 80) return launch_mfma_k<T, OutT, kD, 80>(p, s);
       return launch_mfma_k<T, OutT, kD, 128>(p, s);
     } else {
       return launch_mfma_k<T, OutT, kD, 64>(p, s);
